@@ -1,0 +1,164 @@
+// Shared device/host helpers for the gfx950 kernel set.
+//
+// Everything here is written for CDNA4 wave64: reductions use DPP row
+// operations inside a 16-lane row plus v_readlane across rows, so no LDS
+// round-trip is needed for a row that fits in one wave.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/tpp.h"
+
+namespace tpp {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---- element traits --------------------------------------------------------
+
+template <typename T> struct VecT;
+template <> struct VecT<f16> {
+  typedef f16x8 v8;
+  typedef f16x4 v4;
+  typedef f16x2 v2;
+};
+template <> struct VecT<bf16> {
+  typedef bf16x8 v8;
+  typedef bf16x4 v4;
+  typedef bf16x2 v2;
+};
+
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(float x) { return x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ f16 from_f32<f16>(float x) { return (f16)x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+
+// 16-byte vector load/store of 8 elements, converted to/from fp32.
+template <typename T>
+__device__ __forceinline__ void load8(const T *p, float (&v)[8]) {
+  typedef typename VecT<T>::v8 V;
+  V t = *reinterpret_cast<const V *>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = to_f32(t[i]);
+}
+template <typename T>
+__device__ __forceinline__ void store8(T *p, const float (&v)[8]) {
+  typedef typename VecT<T>::v8 V;
+  V t;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) t[i] = from_f32<T>(v[i]);
+  *reinterpret_cast<V *>(p) = t;
+}
+
+// ---- wave64 reductions -----------------------------------------------------
+// DPP controls (GFX9 encoding): quad_perm, row_half_mirror, row_mirror.
+constexpr int kDppQuadXor1 = 0xB1; // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E; // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over each 16-lane DPP row; every lane of the row receives the row sum.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f32<kDppQuadXor1>(v);
+  v += dpp_f32<kDppQuadXor2>(v);
+  v += dpp_f32<kDppRowHalfMirror>(v);
+  v += dpp_f32<kDppRowMirror>(v);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f32<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dpp_f32<kDppRowMirror>(v));
+  return v;
+}
+
+// Sum over the whole wave; the result is wave-uniform. Requires all 64
+// lanes active (callers keep inactive lanes at 0).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return (readlane_f32(v, 0) + readlane_f32(v, 16)) +
+         (readlane_f32(v, 32) + readlane_f32(v, 48));
+}
+
+// Sum over lanes {l, l^16, l^32, l^48} after a row16 reduction: gives each
+// lane the full-wave value without readlane (used where lane groups differ).
+__device__ __forceinline__ float xor_sum(float v, int mask) {
+  return v + __shfl_xor(v, mask, kWave);
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
+
+// ---- activations (fp32), csrc/activation/activation.cuh:26-67 -------------
+__device__ __forceinline__ float act_gelu_tanh(float x) {
+  const float kAlpha = 0.7978845608028654f; // sqrt(2/pi)
+  const float kBeta = 0.044715f;
+  float t = tanhf(kAlpha * (x + kBeta * x * x * x));
+  return 0.5f * x * (1.0f + t);
+}
+__device__ __forceinline__ float act_silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float act_relu(float x) { return fmaxf(0.0f, x); }
+
+template <int ACT> __device__ __forceinline__ float apply_act(float x) {
+  if constexpr (ACT == TPP_ACT_GELU_TANH) return act_gelu_tanh(x);
+  else if constexpr (ACT == TPP_ACT_SILU) return act_silu(x);
+  else if constexpr (ACT == TPP_ACT_RELU) return act_relu(x);
+  else return x;
+}
+
+// ---- host-side error state -------------------------------------------------
+int set_error(int code, const char *fmt, ...);
+int check_launch(const char *what);
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+inline int elem_size(int dtype) { return dtype == TPP_F32 ? 4 : 2; }
+inline bool half_type(int dtype) { return dtype == TPP_F16 || dtype == TPP_BF16; }
+
+} // namespace tpp
+
+// Dispatch a body over fp16/bf16. `T` names the element type inside.
+#define TPP_DISPATCH_HALF(dtype, ...)                                        \
+  [&]() -> int {                                                             \
+    if ((dtype) == TPP_F16) {                                                \
+      typedef ::tpp::f16 T;                                                  \
+      return __VA_ARGS__();                                                  \
+    } else if ((dtype) == TPP_BF16) {                                        \
+      typedef ::tpp::bf16 T;                                                 \
+      return __VA_ARGS__();                                                  \
+    }                                                                        \
+    return ::tpp::set_error(TPP_E_UNSUPPORTED, "unsupported dtype %d",       \
+                            (int)(dtype));                                   \
+  }()
