@@ -30,7 +30,7 @@ extern "C" {
 typedef enum {
   TPP_F16 = 0,  /* IEEE binary16 (the reference's only type, c10::Half)   */
   TPP_BF16 = 1, /* bfloat16                                               */
-  TPP_F32 = 2   /* float32 (accepted for RoPE cos/sin tables only)        */
+  TPP_F32 = 2   /* float32 (RoPE cos/sin tables only)                     */
 } tpp_dtype;
 
 typedef enum {
@@ -86,6 +86,88 @@ int tpp_layernorm(const void *x, const void *w, const void *b, void *y,
 int tpp_layernorm_stats(const void *x, float *mean, float *rstd, int64_t M,
                         int64_t N, int64_t ldx, float eps, int dtype,
                         void *stream);
+
+/* ---- rotary embedding ---------------------------------------------------- */
+
+/* Rotate-half RoPE on x [B, H, S, D] (contiguous) with tables cos/sin [S, D]
+ * (row s for sequence index s). out may equal x (in place). cs_dtype is the
+ * tables' type (TPP_F16, TPP_BF16 or TPP_F32, independent of dtype; the
+ * reference's compute_rope_params returns fp16). fp32 math, one rounding.
+ * Replaces rope_apply_half2 (csrc/dlops/rope/apply_rope.cuh:49-64), bound as
+ * ropeApplyFunction.rope_apply_cuda (rope_binding.cu:10-67). */
+int tpp_rope(const void *x, void *out, const void *cos, const void *sin,
+             int64_t B, int64_t H, int64_t S, int64_t D, int dtype,
+             int cs_dtype, void *stream);
+
+/* RoPE on q [B, Hq, S, D] and k [B, Hk, S, D] in one launch; Hk may differ
+ * from Hq (GQA). Replaces rope_apply_half2_dual
+ * (csrc/dlops/qkrope/qkrope.cuh:69-93, qkrope_binding.cu:14-92), which
+ * required Hk == Hq. */
+int tpp_rope_qk(const void *q, const void *k, void *q_out, void *k_out,
+                const void *cos, const void *sin, int64_t B, int64_t Hq,
+                int64_t Hk, int64_t S, int64_t D, int dtype, int cs_dtype,
+                void *stream);
+
+/* Fused per-layer attention prologue, replacing the chain at
+ * torchpp/attention/gqa.py:86-118 (q_norm/k_norm RMSNorm over head_dim,
+ * rope_apply on Q and K, KVCache.update at kvcache.py:50-108):
+ *   qkv      [B, S, (Hq + 2*Hkv) * D]  fused projection output
+ *   q_out    [B, S, Hq, D]             normed + rotated queries
+ *   k_cache, v_cache [B, Hkv, Lmax, D] rows pos[b]+s written (K normed+rotated)
+ *   q_norm_w, k_norm_w [D] or NULL (no QK-norm)
+ *   cos, sin [ctx, D] tables indexed by absolute position
+ *   positions int32 [B] device array: first position of each sequence.
+ * D must be 64, 128 or 256. Positions >= Lmax are not written. */
+int tpp_qkv_rope_cache(const void *qkv, void *q_out, void *k_cache,
+                       void *v_cache, const void *q_norm_w,
+                       const void *k_norm_w, const void *cos, const void *sin,
+                       int64_t ctx, const int32_t *positions, int64_t B,
+                       int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
+                       int64_t Lmax, float eps, int dtype, int cs_dtype,
+                       void *stream);
+
+/* ---- linear layers ------------------------------------------------------- */
+
+/* y[M, N] = act(T(x[M, K] . w[N, K]^T + bias)) on MFMA; w is the nn.Linear
+ * weight layout, bias [N] or NULL, act a tpp_act. With act == TPP_ACT_NONE
+ * and bias == NULL this is a plain GEMM. Rounding follows the reference
+ * epilogue: pre-activation rounded to T, activation in fp32.
+ * Replaces linearActvationFp16.LinearGelu/LinearSilu/LinearRelu
+ * (csrc/activation/binding.cu:11-160, CUTLASS GEMM fused_gemm.cuh:143-170). */
+int tpp_linear_act(const void *x, const void *w, const void *bias, void *y,
+                   int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
+                   int act, int dtype, void *stream);
+
+/* Fused gate/up SwiGLU FFN projection, y[M, I] = T(silu(T(g))) * T(u) with
+ * g = x . Wg^T, u = x . Wu^T, from one weight w_gu [2I, K] whose rows are
+ * interleaved in blocks of 32 (rows 64j..64j+31 = Wg rows 32j.., rows
+ * 64j+32..64j+63 = Wu rows 32j..). I % 32 == 0. The eager form is
+ * examples/TTS/dia/model.py:114-116 (silu(gate(x)) * up(x)), which the
+ * reference's FastQwen3 FFN intends (examples/LLM/fastqwen3.py:66-79). */
+int tpp_linear_swiglu(const void *x, const void *w_gu, void *y, int64_t M,
+                      int64_t I, int64_t K, int64_t ldx, int64_t ldy,
+                      int dtype, void *stream);
+
+/* Bytes of zero-initialised workspace tpp_gemv / tpp_gemv_swiglu need for
+ * batch B, N weight rows (2I for swiglu) and K (0 = none). */
+size_t tpp_gemv_workspace_size(int64_t B, int64_t N, int64_t K, int swiglu);
+
+/* Decode GEMV, y[B, N] = act(T(x[B, K] . W[N, K]^T + bias)), B <= 16,
+ * streaming W once for all B rows. workspace: see tpp_gemv_workspace_size; it
+ * must be zero when first used and is left zero by every call, so it can be
+ * reused without clearing; calls sharing it must be stream-ordered.
+ * Replaces hgemvK128F16x4Kernel / launchHgemv
+ * (csrc/blas/hgemv/hgemv_kernels.cuh:19-85), which had no binding. */
+int tpp_gemv(const void *x, const void *W, const void *bias, void *y,
+             int64_t B, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
+             int act, int dtype, void *workspace, size_t ws_bytes,
+             void *stream);
+
+/* Decode SwiGLU GEMV over an interleaved w_gu [2I, K] (layout as in
+ * tpp_linear_swiglu): y[B, I]. */
+int tpp_gemv_swiglu(const void *x, const void *W_gu, void *y, int64_t B,
+                    int64_t I, int64_t K, int64_t ldx, int64_t ldy, int dtype,
+                    void *workspace, size_t ws_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,111 @@
+"""GPU parity: MFMA GEMM + activation epilogue, decode GEMV, SwiGLU."""
+import pytest
+import torch
+
+import oracle
+from tests.conftest import close
+from torchplusplus_amd._native import ext
+from torchplusplus_amd.dlops import linear as L
+
+pytestmark = pytest.mark.gpu
+ACTS = {"none": 0, "gelu": 1, "silu": 2, "relu": 3}
+
+
+def _mk(m, n, k, dtype, seed=0, wstd=0.02):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g).to(dtype)
+    w = (wstd * torch.randn(n, k, generator=g)).to(dtype)
+    b = (wstd * torch.randn(n, generator=g)).to(dtype)
+    return x, w, b
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_linear_silu_baseline_config(dev, dtype):
+    """BASELINE config 2b: [2048x1024] @ [1024x3072] + bias, SiLU."""
+    x, w, b = _mk(2048, 3072, 1024, dtype)
+    y = ext().LinearSilu(x.to(dev), w.to(dev), b.to(dev))
+    close(y, oracle.linear_act(x, w, b, "silu"), what="linear+silu")
+
+
+@pytest.mark.parametrize("act", ["none", "gelu", "silu", "relu"])
+@pytest.mark.parametrize("m,n,k", [(300, 200, 136), (128, 128, 64), (1, 64, 1024), (257, 3, 8)])
+def test_linear_act_shapes(dev, act, m, n, k):
+    x, w, b = _mk(m, n, k, torch.bfloat16, seed=1, wstd=0.1)
+    y = ext().linear(x.to(dev), w.to(dev), b.to(dev), ACTS[act])
+    close(y, oracle.linear_act(x, w, b, act), what=f"linear {act} {m}x{n}x{k}")
+
+
+def test_linear_odd_k_scalar_path(dev):
+    x, w, b = _mk(33, 40, 13, torch.float16, seed=2, wstd=0.2)
+    y = ext().linear(x.to(dev), w.to(dev), None, ACTS["gelu"])
+    close(y, oracle.linear_act(x, w, None, "gelu"), what="odd K")
+
+
+def test_reference_linear_act_test_shape(dev):
+    """tests/linear_act_test.py:5-17: x [32,512], W [256,512] fp16 randn (shape only
+    there); checked here against the formula."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(32, 512, generator=g).half()
+    w = torch.randn(256, 512, generator=g).half()
+    y = ext().LinearSilu(x.to(dev), w.to(dev))
+    assert y.shape == (32, 256)
+    e = oracle.linear_act(x, w, None, "silu")
+    # |acc| ~ sqrt(512) ~ 22: fp16 pre-activation rounding alone is 2^-6 there
+    close(y, e, atol=6e-2, rtol=1e-2, what="randn weights")
+
+
+def test_linear_module_3d_input(dev):
+    mod = L.LinearGELU(256, 512, dtype=torch.bfloat16, device=dev)
+    with torch.no_grad():
+        mod.weight.mul_(0.05)
+    x = torch.randn(4, 100, 256, generator=torch.Generator().manual_seed(4)).bfloat16()
+    y = mod(x.to(dev))
+    assert y.shape == (4, 100, 512)
+    close(y, oracle.linear_act(x, mod.weight.detach().cpu(), None, "gelu"), what="3-D")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bsz", [1, 8, 16])
+@pytest.mark.parametrize("n,k", [(3072, 1024), (1024, 3072), (4096, 1024), (1000, 200), (24, 2048)])
+def test_gemv_parity(dev, dtype, bsz, n, k):
+    """[1x1024]@[1024x3072] and [1x3072]@[3072x1024]; plus the
+    decode-step shapes at batch 8/16 and ragged sizes (split-K workspace paths)."""
+    x, w, _ = _mk(bsz, n, k, dtype, seed=5)
+    y = ext().gemv(x.to(dev), w.to(dev))
+    close(y, oracle.gemv(x, w), what=f"gemv b{bsz} {n}x{k}")
+
+
+def test_gemv_repeated_calls_keep_workspace_clean(dev):
+    """The split-K workspace is self-cleaning: many calls in a row, same result."""
+    x, w, _ = _mk(8, 1024, 3072, torch.bfloat16, seed=6)
+    xd, wd = x.to(dev), w.to(dev)
+    first = ext().gemv(xd, wd)
+    for _ in range(20):
+        again = ext().gemv(xd, wd)
+    assert torch.equal(first, again)
+    close(first, oracle.gemv(x, w), what="repeat")
+
+
+def test_gemv_bias_act_and_hgemv_cpu_reference(dev):
+    import numpy as np
+
+    x, w, b = _mk(1, 512, 1024, torch.float16, seed=7)
+    y = ext().gemv(x.to(dev), w.to(dev), b.to(dev), ACTS["silu"])
+    close(y, oracle.linear_act(x, w, b, "silu"), what="gemv silu")
+    y0 = ext().gemv(x.to(dev), w.to(dev))
+    ref = oracle.hgemv_cpu(w.numpy(), x[0].numpy())
+    close(y0[0], torch.from_numpy(ref), what="vs hgemvCpu restatement")
+
+
+@pytest.mark.parametrize("rows", [1, 8, 300])
+def test_swiglu_gemm_and_gemv(dev, rows):
+    g = torch.Generator().manual_seed(8)
+    I, K = 3072, 1024
+    x = torch.randn(rows, K, generator=g).bfloat16()
+    wg = (0.02 * torch.randn(I, K, generator=g)).bfloat16()
+    wu = (0.02 * torch.randn(I, K, generator=g)).bfloat16()
+    wgu = L.interleave_gate_up(wg, wu)
+    y = L.swiglu(x.to(dev), wgu.to(dev))
+    gt = oracle.linear_act(x, wg)
+    e = (torch.nn.functional.silu(gt.float()).bfloat16().float() * oracle.linear_act(x, wu).float()).bfloat16()
+    close(y, e, what=f"swiglu rows={rows}")

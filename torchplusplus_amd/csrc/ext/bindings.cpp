@@ -161,9 +161,261 @@ std::vector<at::Tensor> layernorm_stats(at::Tensor input, double eps) {
   return {mean, rstd};
 }
 
+// ---- RoPE (rope_binding.cu:10-67, qkrope_binding.cu:14-92) -----------------
+void check_rope_tables(const at::Tensor &x, const at::Tensor &cos_cache,
+                       const at::Tensor &sin_cache, int64_t N, int64_t D) {
+  TORCH_CHECK(cos_cache.device().is_cuda(), "cos_cache tensor must be on CUDA device");
+  TORCH_CHECK(sin_cache.device().is_cuda(), "sin_cache tensor must be on CUDA device");
+  TORCH_CHECK(dtype_code(cos_cache) >= 0,
+              "cos_cache tensor must be float16, bfloat16 or float32");
+  TORCH_CHECK(sin_cache.scalar_type() == cos_cache.scalar_type(),
+              "sin_cache tensor must have cos_cache's dtype");
+  TORCH_CHECK(cos_cache.is_contiguous(), "cos_cache tensor must be contiguous");
+  TORCH_CHECK(sin_cache.is_contiguous(), "sin_cache tensor must be contiguous");
+  TORCH_CHECK(cos_cache.dim() == 2, "cos_cache must be 2D [seq_len, head_dim]");
+  TORCH_CHECK(sin_cache.dim() == 2, "sin_cache must be 2D [seq_len, head_dim]");
+  TORCH_CHECK(cos_cache.size(0) == N && cos_cache.size(1) == D, "cos_cache shape mismatch");
+  TORCH_CHECK(sin_cache.size(0) == N && sin_cache.size(1) == D, "sin_cache shape mismatch");
+}
+
+at::Tensor rope_apply_impl(at::Tensor x, at::Tensor cos_cache, at::Tensor sin_cache,
+                           bool inplace) {
+  TORCH_CHECK(x.device().is_cuda(), "Input tensor must be on CUDA device");
+  TORCH_CHECK(is_half_or_bf16(x), "Input tensor must be float16 or bfloat16");
+  TORCH_CHECK(x.is_contiguous(), "Input tensor must be contiguous");
+  TORCH_CHECK(x.dim() == 4, "Input tensor must be 4D [batch, heads, seq_len, head_dim]");
+  const int64_t B = x.size(0), H = x.size(1), N = x.size(2), D = x.size(3);
+  TORCH_CHECK(D % 2 == 0, "head dim must be even");
+  check_rope_tables(x, cos_cache, sin_cache, N, D);
+  c10::DeviceGuard g(x.device());
+  at::Tensor out = inplace ? x : torch::empty_like(x);
+  check_rc(tpp_rope(x.data_ptr(), out.data_ptr(), cos_cache.data_ptr(), sin_cache.data_ptr(),
+                    B, H, N, D, dtype_code(x), dtype_code(cos_cache), cur_stream(x)),
+           "rope_apply_cuda");
+  return out;
+}
+
+at::Tensor rope_apply_cuda(at::Tensor x, at::Tensor cos_cache, at::Tensor sin_cache) {
+  return rope_apply_impl(x, cos_cache, sin_cache, false);
+}
+at::Tensor rope_apply_inplace(at::Tensor x, at::Tensor cos_cache, at::Tensor sin_cache) {
+  return rope_apply_impl(x, cos_cache, sin_cache, true);
+}
+
+std::vector<at::Tensor> qkrope_apply_cuda(at::Tensor q, at::Tensor k, at::Tensor cos_cache,
+                                          at::Tensor sin_cache) {
+  TORCH_CHECK(q.device().is_cuda(), "Query tensor must be on CUDA device");
+  TORCH_CHECK(is_half_or_bf16(q), "Query tensor must be float16 or bfloat16");
+  TORCH_CHECK(q.is_contiguous(), "Query tensor must be contiguous");
+  TORCH_CHECK(k.device().is_cuda(), "Key tensor must be on CUDA device");
+  TORCH_CHECK(k.scalar_type() == q.scalar_type(), "Key tensor must have the query dtype");
+  TORCH_CHECK(k.is_contiguous(), "Key tensor must be contiguous");
+  TORCH_CHECK(q.dim() == 4, "Query tensor must be 4D [batch, heads, seq_len, head_dim]");
+  TORCH_CHECK(k.dim() == 4, "Key tensor must be 4D [batch, heads, seq_len, head_dim]");
+  const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
+  TORCH_CHECK(D % 2 == 0, "head_dim must be even");
+  TORCH_CHECK(k.size(0) == B, "Key batch size must match query");
+  TORCH_CHECK(k.size(1) <= H && H % k.size(1) == 0,
+              "Key num_heads must divide query num_heads (GQA)");
+  TORCH_CHECK(k.size(2) == N, "Key seq_len must match query");
+  TORCH_CHECK(k.size(3) == D, "Key head_dim must match query");
+  check_rope_tables(q, cos_cache, sin_cache, N, D);
+  c10::DeviceGuard g(q.device());
+  auto qo = torch::empty_like(q);
+  auto ko = torch::empty_like(k);
+  check_rc(tpp_rope_qk(q.data_ptr(), k.data_ptr(), qo.data_ptr(), ko.data_ptr(),
+                       cos_cache.data_ptr(), sin_cache.data_ptr(), B, H, k.size(1), N, D,
+                       dtype_code(q), dtype_code(cos_cache), cur_stream(q)),
+           "qkrope_apply_cuda");
+  return {qo, ko};
+}
+
+void qkv_rope_cache(at::Tensor qkv, at::Tensor q_out, at::Tensor k_cache, at::Tensor v_cache,
+                    c10::optional<at::Tensor> q_norm_w, c10::optional<at::Tensor> k_norm_w,
+                    at::Tensor cos, at::Tensor sin, at::Tensor positions, double eps) {
+  TORCH_CHECK(qkv.is_cuda() && qkv.is_contiguous() && is_half_or_bf16(qkv),
+              "qkv must be a contiguous CUDA half/bfloat16 tensor [B, S, (Hq+2Hkv)*D]");
+  TORCH_CHECK(q_out.dim() == 4 && q_out.is_contiguous() &&
+                  q_out.scalar_type() == qkv.scalar_type(),
+              "q_out must be contiguous [B, S, Hq, D]");
+  TORCH_CHECK(k_cache.dim() == 4 && k_cache.is_contiguous() && v_cache.is_contiguous() &&
+                  k_cache.sizes() == v_cache.sizes() &&
+                  k_cache.scalar_type() == qkv.scalar_type() &&
+                  v_cache.scalar_type() == qkv.scalar_type(),
+              "caches must be contiguous [B, Hkv, Lmax, D] of the qkv dtype");
+  TORCH_CHECK(positions.is_cuda() && positions.scalar_type() == at::kInt &&
+                  positions.numel() == q_out.size(0),
+              "positions must be a CUDA int32 tensor of length B");
+  const int64_t B = q_out.size(0), S = q_out.size(1), Hq = q_out.size(2), D = q_out.size(3);
+  const int64_t Hkv = k_cache.size(1), Lmax = k_cache.size(2);
+  TORCH_CHECK(k_cache.size(0) == B && k_cache.size(3) == D, "cache shape mismatch");
+  TORCH_CHECK(qkv.numel() == B * S * (Hq + 2 * Hkv) * D, "qkv size mismatch");
+  TORCH_CHECK(cos.is_contiguous() && sin.is_contiguous() && cos.dim() == 2 &&
+                  cos.size(1) == D && sin.sizes() == cos.sizes() &&
+                  sin.scalar_type() == cos.scalar_type(),
+              "cos/sin must be contiguous [ctx, D] tables");
+  const void *qw = nullptr, *kw = nullptr;
+  if (q_norm_w.has_value() && q_norm_w->defined()) {
+    TORCH_CHECK(q_norm_w->numel() == D && q_norm_w->scalar_type() == qkv.scalar_type() &&
+                    q_norm_w->is_contiguous(),
+                "q_norm weight must be [D] of the qkv dtype");
+    qw = q_norm_w->data_ptr();
+  }
+  if (k_norm_w.has_value() && k_norm_w->defined()) {
+    TORCH_CHECK(k_norm_w->numel() == D && k_norm_w->scalar_type() == qkv.scalar_type() &&
+                    k_norm_w->is_contiguous(),
+                "k_norm weight must be [D] of the qkv dtype");
+    kw = k_norm_w->data_ptr();
+  }
+  c10::DeviceGuard g(qkv.device());
+  check_rc(tpp_qkv_rope_cache(qkv.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(),
+                              v_cache.data_ptr(), qw, kw, cos.data_ptr(), sin.data_ptr(),
+                              cos.size(0), positions.data_ptr<int32_t>(), B, S, Hq, Hkv, D,
+                              Lmax, (float)eps, dtype_code(qkv), dtype_code(cos),
+                              cur_stream(qkv)),
+           "qkv_rope_cache");
+}
+
+// ---- Linear + activation (binding.cu:11-160) --------------------------------
+void check_linear(const at::Tensor &input, const at::Tensor &weight) {
+  TORCH_CHECK(input.dim() >= 1, "Input must be at least 1D");
+  TORCH_CHECK(weight.dim() == 2, "Weight must be 2D");
+  TORCH_CHECK(input.size(input.dim() - 1) == weight.size(1), "Dimension mismatch");
+  TORCH_CHECK(is_half_or_bf16(input), "Input must be FP16 or BF16");
+  TORCH_CHECK(weight.scalar_type() == input.scalar_type(), "Weight must have the input dtype");
+  TORCH_CHECK(input.is_cuda(), "Input must be on CUDA");
+  TORCH_CHECK(weight.is_cuda(), "Weight must be on CUDA");
+  TORCH_CHECK(input.is_contiguous(), "Input must be contiguous");
+  TORCH_CHECK(weight.is_contiguous(), "Weight must be contiguous");
+}
+
+const void *bias_ptr(const c10::optional<at::Tensor> &bias, const at::Tensor &input,
+                     int64_t N) {
+  if (!bias.has_value() || !bias->defined()) return nullptr;
+  TORCH_CHECK(bias->is_cuda() && bias->scalar_type() == input.scalar_type() &&
+                  bias->is_contiguous() && bias->numel() == N,
+              "bias must be a contiguous CUDA tensor [N] of the input dtype");
+  return bias->data_ptr();
+}
+
+std::vector<int64_t> out_shape(const at::Tensor &input, int64_t N) {
+  auto s = input.sizes().vec();
+  s.back() = N;
+  return s;
+}
+
+at::Tensor linear_act(at::Tensor input, at::Tensor weight, c10::optional<at::Tensor> bias,
+                      int64_t act) {
+  check_linear(input, weight);
+  const int64_t K = weight.size(1), N = weight.size(0), M = input.numel() / K;
+  const void *bp = bias_ptr(bias, input, N);
+  c10::DeviceGuard g(input.device());
+  auto out = torch::empty(out_shape(input, N), input.options());
+  check_rc(tpp_linear_act(input.data_ptr(), weight.data_ptr(), bp, out.data_ptr(), M, N, K, K,
+                          N, (int)act, dtype_code(input), cur_stream(input)),
+           "linear_act");
+  return out;
+}
+
+at::Tensor linear_gelu(at::Tensor i, at::Tensor w, c10::optional<at::Tensor> b) {
+  return linear_act(i, w, b, TPP_ACT_GELU_TANH);
+}
+at::Tensor linear_silu(at::Tensor i, at::Tensor w, c10::optional<at::Tensor> b) {
+  return linear_act(i, w, b, TPP_ACT_SILU);
+}
+at::Tensor linear_relu(at::Tensor i, at::Tensor w, c10::optional<at::Tensor> b) {
+  return linear_act(i, w, b, TPP_ACT_RELU);
+}
+
+at::Tensor linear_swiglu(at::Tensor input, at::Tensor w_gu) {
+  check_linear(input, w_gu);
+  const int64_t K = w_gu.size(1), I = w_gu.size(0) / 2, M = input.numel() / K;
+  TORCH_CHECK(w_gu.size(0) % 64 == 0, "w_gu rows must be a multiple of 64");
+  c10::DeviceGuard g(input.device());
+  auto out = torch::empty(out_shape(input, I), input.options());
+  check_rc(tpp_linear_swiglu(input.data_ptr(), w_gu.data_ptr(), out.data_ptr(), M, I, K, K, I,
+                             dtype_code(input), cur_stream(input)),
+           "linear_swiglu");
+  return out;
+}
+
+// Per-device zeroed GEMV workspace, reused (the kernels leave it zero).
+at::Tensor gemv_workspace(const at::Tensor &like, size_t bytes) {
+  // intentionally leaked: no tensor destructor runs after the allocator is gone
+  static std::vector<at::Tensor> *cache = new std::vector<at::Tensor>(64);
+  const int dev = like.device().index();
+  TORCH_CHECK(dev >= 0 && dev < 64, "device index out of range");
+  at::Tensor &ws = (*cache)[dev];
+  if (bytes == 0) bytes = 16;
+  if (!ws.defined() || (size_t)ws.numel() * 4 < bytes) {
+    size_t n = (bytes + 3) / 4;
+    n = n < (1u << 20) ? (1u << 20) : n; // at least 4 MiB
+    ws = torch::zeros({(int64_t)n}, like.options().dtype(at::kFloat));
+  }
+  return ws;
+}
+
+at::Tensor gemv(at::Tensor input, at::Tensor weight, c10::optional<at::Tensor> bias,
+                int64_t act) {
+  check_linear(input, weight);
+  const int64_t K = weight.size(1), N = weight.size(0), B = input.numel() / K;
+  TORCH_CHECK(B >= 1 && B <= 16, "gemv supports 1..16 input rows, got ", B);
+  const void *bp = bias_ptr(bias, input, N);
+  c10::DeviceGuard g(input.device());
+  auto out = torch::empty(out_shape(input, N), input.options());
+  const size_t wsb = tpp_gemv_workspace_size(B, N, K, 0);
+  at::Tensor ws = gemv_workspace(input, wsb);
+  check_rc(tpp_gemv(input.data_ptr(), weight.data_ptr(), bp, out.data_ptr(), B, N, K, K, N,
+                    (int)act, dtype_code(input), ws.data_ptr(), (size_t)ws.numel() * 4,
+                    cur_stream(input)),
+           "gemv");
+  return out;
+}
+
+at::Tensor gemv_swiglu(at::Tensor input, at::Tensor w_gu) {
+  check_linear(input, w_gu);
+  const int64_t K = w_gu.size(1), I = w_gu.size(0) / 2, B = input.numel() / K;
+  TORCH_CHECK(B >= 1 && B <= 16, "gemv supports 1..16 input rows, got ", B);
+  TORCH_CHECK(w_gu.size(0) % 64 == 0, "w_gu rows must be a multiple of 64");
+  c10::DeviceGuard g(input.device());
+  auto out = torch::empty(out_shape(input, I), input.options());
+  const size_t wsb = tpp_gemv_workspace_size(B, 2 * I, K, 1);
+  at::Tensor ws = gemv_workspace(input, wsb);
+  check_rc(tpp_gemv_swiglu(input.data_ptr(), w_gu.data_ptr(), out.data_ptr(), B, I, K, K, I,
+                           dtype_code(input), ws.data_ptr(), (size_t)ws.numel() * 4,
+                           cur_stream(input)),
+           "gemv_swiglu");
+  return out;
+}
+
 } // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("rope_apply_cuda", &rope_apply_cuda, "RoPE (rotate-half), out of place",
+        py::arg("x"), py::arg("cos_cache"), py::arg("sin_cache"));
+  m.def("rope_apply_", &rope_apply_inplace, "RoPE (rotate-half), in place", py::arg("x"),
+        py::arg("cos_cache"), py::arg("sin_cache"));
+  m.def("qkrope_apply_cuda", &qkrope_apply_cuda, "RoPE on Q and K in one launch (Hk | Hq)",
+        py::arg("q"), py::arg("k"), py::arg("cos_cache"), py::arg("sin_cache"));
+  m.def("qkv_rope_cache", &qkv_rope_cache,
+        "fused QK-RMSNorm + RoPE + KV-cache append of a fused qkv projection", py::arg("qkv"),
+        py::arg("q_out"), py::arg("k_cache"), py::arg("v_cache"), py::arg("q_norm_w"),
+        py::arg("k_norm_w"), py::arg("cos"), py::arg("sin"), py::arg("positions"),
+        py::arg("eps") = 1e-6);
+  m.def("LinearGelu", &linear_gelu, "Linear + GeLU(tanh) (fp16/bf16, MFMA)", py::arg("input"),
+        py::arg("weight"), py::arg("bias") = py::none());
+  m.def("LinearSilu", &linear_silu, "Linear + SiLU (fp16/bf16, MFMA)", py::arg("input"),
+        py::arg("weight"), py::arg("bias") = py::none());
+  m.def("LinearRelu", &linear_relu, "Linear + ReLU (fp16/bf16, MFMA)", py::arg("input"),
+        py::arg("weight"), py::arg("bias") = py::none());
+  m.def("linear", &linear_act, "act(x @ W^T + b), act: 0 none,1 gelu_tanh,2 silu,3 relu",
+        py::arg("input"), py::arg("weight"), py::arg("bias") = py::none(), py::arg("act") = 0);
+  m.def("linear_swiglu", &linear_swiglu, "silu(x Wg^T) * (x Wu^T) from interleaved w_gu",
+        py::arg("input"), py::arg("w_gu"));
+  m.def("gemv", &gemv, "decode GEMV for <= 16 rows", py::arg("input"), py::arg("weight"),
+        py::arg("bias") = py::none(), py::arg("act") = 0);
+  m.def("gemv_swiglu", &gemv_swiglu, "decode SwiGLU GEMV for <= 16 rows", py::arg("input"),
+        py::arg("w_gu"));
   m.doc() = "torchpp gfx950 kernel set (binding over libtorchpp_hip.so)";
   m.def("rmsnormFused", &rmsnorm_fused, "Fused RMSNorm (fp16/bf16)", py::arg("input"),
         py::arg("weight"), py::arg("eps") = 1e-6);
