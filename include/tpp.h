@@ -169,6 +169,54 @@ int tpp_gemv_swiglu(const void *x, const void *W_gu, void *y, int64_t B,
                     int64_t I, int64_t K, int64_t ldx, int64_t ldy, int dtype,
                     void *workspace, size_t ws_bytes, void *stream);
 
+/* ---- attention ----------------------------------------------------------- */
+
+/* Flash attention forward, the flash_attn_func contract used by the reference
+ * (torchpp/attention/gqa.py:128, swa.py:85-89, mha.py:84, mqa.py:87,
+ * ca.py:83; the in-repo csrc/attention/flash_attn.cuh:35-604 is an unbound
+ * MHA-only spec):
+ *   q, o [B, Sq, Hq, D]; k, v [B, Sk, Hkv, D]; each *_strides is
+ *   {batch, seq, head} in elements, last dim contiguous. Hq % Hkv == 0
+ *   (GQA/MQA). softmax_scale <= 0 means 1/sqrt(D). causal is aligned
+ *   bottom-right; window_left/right < 0 = unbounded (causal forces right = 0).
+ *   Rows with no visible key are 0. D <= 256; D in {64, 128} with 16-byte
+ *   aligned strides runs the MFMA kernel, other shapes a slow generic one. */
+int tpp_attn_prefill(const void *q, const void *k, const void *v, void *o,
+                     const int64_t *q_strides, const int64_t *k_strides,
+                     const int64_t *v_strides, const int64_t *o_strides,
+                     int64_t B, int64_t Sq, int64_t Sk, int64_t Hq,
+                     int64_t Hkv, int64_t D, float softmax_scale, int causal,
+                     int window_left, int window_right, int dtype,
+                     void *stream);
+
+/* Bytes of workspace tpp_attn_decode needs (no initialisation required). */
+size_t tpp_attn_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv,
+                                      int64_t D, int64_t Lmax);
+
+/* Split-KV decode attention: one query per sequence (q, o [B, 1, Hq, D]
+ * through {batch, -, head} strides) against the first seqlens[b] keys of a
+ * KV cache addressed by {batch, position, head} strides (the KVCache layout
+ * [B, Hkv, Lmax, D] of torchpp/llmops/kvcache.py:39-48, batch-generalised).
+ * seqlens: int32 [B] on the device, or NULL for Lmax keys everywhere.
+ * window_left >= 0 keeps keys >= L-1-window_left. D in {64, 128},
+ * Hq/Hkv <= 8. Replaces flash_attn_func with Sq = 1 over the cache prefix
+ * (gqa.py:117-128). */
+int tpp_attn_decode(const void *q, const void *k_cache, const void *v_cache,
+                    void *o, const int64_t *q_strides, const int64_t *k_strides,
+                    const int64_t *v_strides, const int64_t *o_strides,
+                    const int32_t *seqlens, int64_t B, int64_t Hq, int64_t Hkv,
+                    int64_t D, int64_t Lmax, float softmax_scale,
+                    int window_left, int dtype, void *workspace,
+                    size_t ws_bytes, void *stream);
+
+/* ---- sampling ------------------------------------------------------------ */
+
+/* Greedy sampling: out[b] = argmax_n x[b, n] for x [B, ldx] (first index of
+ * the maximum, NaN is the maximum), as torch.argmax in
+ * LLMInference.sample_greedy (torchpp/llmops/llm.py:181-186). */
+int tpp_argmax_rows(const void *x, int64_t *out, int64_t B, int64_t N,
+                    int64_t ldx, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

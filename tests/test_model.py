@@ -1,0 +1,80 @@
+"""GPU parity of the FastQwen3 decoder vs the CPU model oracle (tiny config),
+teacher-forced decode through the KV cache, and graph vs eager greedy decode."""
+import pytest
+import torch
+
+from oracle.qwen3 import Qwen3Oracle
+from tests.conftest import close
+from torchplusplus_amd.fastqwen3 import FastQwen3, GreedyDecoder, QwenConfig
+
+pytestmark = pytest.mark.gpu
+
+TINY = QwenConfig(vocab_size=1000, context_length=512, embed_dim=256, n_heads=4, n_layers=2,
+                  head_dim=128, n_kv_heads=2, hidden_dim=512, dtype=torch.bfloat16)
+
+
+def _model(dev, cfg=TINY, seed=0):
+    torch.manual_seed(seed)
+    m = FastQwen3(cfg, device=dev).eval()
+    g = torch.Generator(device=dev).manual_seed(seed)
+    m.init_weights(std=0.05, generator=g)
+    with torch.no_grad():  # non-trivial norm weights
+        for n, p in m.named_parameters():
+            if "norm" in n:
+                p.copy_(1 + 0.1 * torch.randn(p.shape, generator=g, device=dev).to(p.dtype))
+    return m
+
+
+@torch.inference_mode()
+def test_prefill_and_teacher_forced_decode(dev):
+    m = _model(dev)
+    orc = Qwen3Oracle(m.state_dict(), TINY, TINY.context_length)
+    B, S = 3, 40
+    ids = torch.randint(0, TINY.vocab_size, (B, S + 4), generator=torch.Generator().manual_seed(1))
+    m.setup_kv_cache(64, B)
+    m.reset_kv_cache()
+    got = m.forward(ids[:, :S].to(dev), use_cache=True, cache_position=0)
+    exp = orc.forward(ids[:, :S], 0)
+    close(got, exp, atol=3e-2, rtol=2e-2, what="prefill logits")
+    for t in range(4):  # decode with the true next token (teacher forcing)
+        got = m.forward(ids[:, S + t:S + t + 1].to(dev), use_cache=True, cache_position=S + t)
+        exp = orc.forward(ids[:, S + t:S + t + 1], S + t)
+        close(got, exp, atol=3e-2, rtol=2e-2, what=f"decode step {t}")
+
+
+@torch.inference_mode()
+def test_forward_without_cache_matches_cached_prefill(dev):
+    m = _model(dev, seed=2)
+    ids = torch.randint(0, TINY.vocab_size, (2, 33), generator=torch.Generator().manual_seed(3)).to(dev)
+    a = m(ids)
+    m.setup_kv_cache(64, 2)
+    m.reset_kv_cache()
+    b = m(ids, use_cache=True, cache_position=0)
+    close(a, b, atol=1e-2, rtol=1e-2, what="no-cache vs cache prefill")
+
+
+@torch.inference_mode()
+def test_graph_decode_equals_eager_decode(dev):
+    m = _model(dev, seed=4)
+    B, S, N = 4, 17, 12
+    ids = torch.randint(0, TINY.vocab_size, (B, S), generator=torch.Generator().manual_seed(5)).to(dev)
+    eager = m.generate_greedy(ids, N, use_graph=False)
+    graph = m.generate_greedy(ids, N, use_graph=True)
+    assert torch.equal(eager, graph)
+    # the reference-style generate() loop gives the same greedy tokens
+    ref_style = m.generate(ids, max_new_token=N, sampling_strategy="greedy")
+    assert torch.equal(ref_style, eager)
+
+
+@torch.inference_mode()
+def test_graph_replays_are_stable(dev):
+    """Graph replays interleaved with eager work must match a fresh eager run."""
+    m = _model(dev, seed=6)
+    B, S = 2, 9
+    ids = torch.randint(0, TINY.vocab_size, (B, S), generator=torch.Generator().manual_seed(7)).to(dev)
+    want = m.generate_greedy(ids, 8, use_graph=False)
+    for _ in range(3):
+        _ = torch.randn(1000, device=dev).sum()  # unrelated eager work between runs
+        got = m.generate_greedy(ids, 8, use_graph=True)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)

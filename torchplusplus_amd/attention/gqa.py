@@ -1,0 +1,101 @@
+"""Grouped-query attention (reference: torchpp/attention/gqa.py:11-131).
+
+Same constructor and forward signature. Per call the layer runs:
+  1. one fused Q/K/V projection (MFMA GEMM, or the split-K GEMV for <= 16 tokens)
+  2. one fused kernel: QK-RMSNorm over head_dim + RoPE at the absolute
+     positions + K/V written into the cache (or a scratch buffer)
+  3. flash attention with native GQA (no repeat_interleave / .contiguous()
+     copies), or split-KV decode attention when a single token is appended
+  4. the output projection.
+The fused projection weight is built from Wq/Wk/Wv on first use; call
+`refresh_fused_weights()` after changing those parameters.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from torchplusplus_amd._native import ext as _ext
+from torchplusplus_amd.attention.flash import decode_attention, flash_attn_func
+from torchplusplus_amd.dlops.linear import linear
+from torchplusplus_amd.llmops.kvcache import KVCache
+
+_C = _ext()
+
+
+class GroupedQueryAttention(nn.Module):
+    def __init__(self, d_in: int, num_heads: int, n_kv_heads: int, head_dim: Optional[int] = None,
+                 qk_norm: bool = True, dtype: torch.dtype = torch.float16, DEBUG: bool = False,
+                 device=None):
+        super().__init__()
+        assert num_heads % n_kv_heads == 0, "Num heads is not divisible by num kv grps"
+        self.num_heads = num_heads
+        self.n_kv_heads = n_kv_heads
+        self.num_kv_grps = num_heads // n_kv_heads
+        if head_dim is None:
+            assert d_in % num_heads == 0, "in dimension must be divisible by number of heads"
+            head_dim = d_in // num_heads
+        self.head_dim = head_dim
+        self.d_out = head_dim * num_heads
+        kw = dict(bias=False, dtype=dtype, device=device)
+        self.Wq = nn.Linear(d_in, self.d_out, **kw)
+        self.Wk = nn.Linear(d_in, n_kv_heads * head_dim, **kw)
+        self.Wv = nn.Linear(d_in, n_kv_heads * head_dim, **kw)
+        self.out_projection = nn.Linear(self.d_out, d_in, **kw)
+        if qk_norm:
+            self.q_norm = nn.RMSNorm(head_dim, eps=1e-6, dtype=dtype, device=device)
+            self.k_norm = nn.RMSNorm(head_dim, eps=1e-6, dtype=dtype, device=device)
+        else:
+            self.q_norm = self.k_norm = None
+        self.DEBUG = DEBUG
+        self._wqkv = None
+
+    def refresh_fused_weights(self):
+        with torch.no_grad():
+            self._wqkv = torch.cat([self.Wq.weight, self.Wk.weight, self.Wv.weight], 0).contiguous()
+
+    def fused_qkv_weight(self) -> torch.Tensor:
+        if self._wqkv is None or self._wqkv.device != self.Wq.weight.device:
+            self.refresh_fused_weights()
+        return self._wqkv
+
+    def project_rope_cache(self, x, cos, sin, k_dst, v_dst, positions):
+        """Steps 1-2: returns q [B, S, Hq, D]; K/V rows land in k_dst/v_dst
+        ([B, Hkv, L, D]) at positions[b] + s."""
+        bs, seq_len, _ = x.shape
+        qkv = linear(x, self.fused_qkv_weight())
+        q = torch.empty(bs, seq_len, self.num_heads, self.head_dim, dtype=x.dtype, device=x.device)
+        eps = self.q_norm.eps if self.q_norm is not None else 1e-6
+        _C.qkv_rope_cache(qkv, q, k_dst, v_dst,
+                          self.q_norm.weight if self.q_norm is not None else None,
+                          self.k_norm.weight if self.k_norm is not None else None,
+                          cos, sin, positions, eps if eps is not None else 1e-6)
+        return q
+
+    def forward(self, x, cos, sin, kv_cache: Optional[KVCache] = None,
+                cache_pos: Optional[int] = None):
+        bs, seq_len, _ = x.shape
+        dev = x.device
+        if kv_cache is not None:
+            start = kv_cache.cache_len if cache_pos is None else int(cache_pos)
+            kv_cache.ensure(bs, start + seq_len)
+            positions = torch.full((bs,), start, dtype=torch.int32, device=dev)
+            q = self.project_rope_cache(x, cos, sin, kv_cache.k_cache, kv_cache.v_cache, positions)
+            kv_cache.cache_len = max(kv_cache.cache_len, start + seq_len)
+            total = start + seq_len
+            if seq_len == 1:
+                seqlens = torch.full((bs,), total, dtype=torch.int32, device=dev)
+                o = decode_attention(q, kv_cache.k_cache, kv_cache.v_cache, seqlens)
+            else:
+                kc = kv_cache.k_cache[:bs, :, :total].transpose(1, 2)
+                vc = kv_cache.v_cache[:bs, :, :total].transpose(1, 2)
+                o = flash_attn_func(q, kc, vc, causal=True)
+        else:
+            k = torch.empty(bs, self.n_kv_heads, seq_len, self.head_dim, dtype=x.dtype, device=dev)
+            v = torch.empty_like(k)
+            positions = torch.zeros(bs, dtype=torch.int32, device=dev)
+            q = self.project_rope_cache(x, cos, sin, k, v, positions)
+            o = flash_attn_func(q, k.transpose(1, 2), v.transpose(1, 2), causal=True)
+        return linear(o.reshape(bs, seq_len, self.d_out), self.out_projection.weight)

@@ -1,0 +1,667 @@
+// Flash attention for gfx950: GQA/MQA/MHA, causal and sliding-window prefill,
+// and split-KV decode against a KV cache.
+//
+// Contract: the flash_attn_func calls of the reference
+// (torchpp/attention/gqa.py:128, swa.py:85-89, mha.py:84, mqa.py:87, ca.py:83):
+//   O = softmax(Q K^T * scale + mask) V, fp32 softmax and accumulation,
+//   scale = 1/sqrt(D) by default, query head h reads KV head h / (Hq/Hkv),
+//   causal aligned bottom-right (key j visible to query i iff
+//   j <= i + Sk - Sq), window (left, right) keeps
+//   i + Sk - Sq - left <= j <= i + Sk - Sq + right (negative = unbounded),
+//   a query with no visible key yields O = 0.
+// Layout: q/o [B, S, H, D] and k/v [B, S, Hkv, D] with arbitrary batch/seq/
+// head strides and a contiguous last dim (flash-attn's layout); the KV cache
+// of the decode path is [B, Hkv, Lmax, D] through the same strides.
+//
+// Prefill kernel (D = 64 or 128): one wave = 32 queries of one head.
+//  * S^T = K . Q^T with v_mfma_f32_32x32x16 (K tile from LDS as operand A,
+//    the wave's Q kept in VGPRs as operand B), so every lane owns ONE query
+//    and 32 of the 64 scores of a KV tile: the softmax max/sum is an in-lane
+//    loop plus a single exchange with lane ^ 32.
+//  * O^T += V^T . P^T: P never leaves registers. MFMA operands pair lane half
+//    h and element j with a K index; choosing key(c, h, j) =
+//    16c + 8(j/4) + 4h + j%4 for the c-th 16-key step makes the score
+//    registers of S^T exactly the B operand, and the A operand two 8-byte LDS
+//    reads of a transposed V tile.
+//  * K and V^T tiles are staged through XOR-swizzled LDS (16-byte chunks for
+//    K, 8-byte 4-key slots for V^T), double-buffered, one barrier per tile.
+//  * A block is 4 waves over the query heads that share one KV head (GQA),
+//    so a K/V tile in LDS serves up to 4 heads; causal/window tiles outside
+//    the block's band are skipped, masks are evaluated only on band edges,
+//    and the heaviest (latest) query tiles are dispatched first.
+// Decode kernel: a block = (batch, KV head, key chunk); each 16-lane DPP row
+// (D/8 lanes) handles one key, all query heads of the group are scored
+// against it, online softmax per lane, then log-sum-exp merges across rows,
+// waves (LDS) and chunks (a second small kernel).
+#include "tpp_common.hpp"
+
+namespace tpp {
+
+struct AttnArgs {
+  const void *q, *k, *v;
+  void *o;
+  int64_t q_sb, q_ss, q_sh;
+  int64_t k_sb, k_ss, k_sh;
+  int64_t v_sb, v_ss, v_sh;
+  int64_t o_sb, o_ss, o_sh;
+  int B, Sq, Sk, Hq, Hkv;
+  float scale_log2; // softmax scale * log2(e)
+  int left, right;  // window, -1 = unbounded; causal => right = 0
+};
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kKvTile = 64;
+
+template <typename T>
+__device__ __forceinline__ f32x16 mfma32x32(typename VecT<T>::v8 a, typename VecT<T>::v8 b,
+                                            f32x16 c) {
+  if constexpr (__is_same(T, bf16))
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int vt_swz(int d) { return (d ^ (d >> 3)) & 15; }
+
+template <typename T, int D> struct PrefillSmem {
+  typedef typename VecT<T>::v8 V8;
+  V8 k[2][kKvTile * D / 8];  // [key][chunk ^ (key % (D/8))]
+  uint64_t vt[2][D * 16];    // [d][slot ^ vt_swz(d)], slot = 4 keys
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs p, int hpb) {
+  typedef typename VecT<T>::v8 V8;
+  constexpr int CPR = D / 8; // 16-byte chunks per row
+  constexpr int NT = D / 32; // 32-row MFMA tiles along D
+  __shared__ PrefillSmem<T, D> sm;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = lane >> 5, ql = lane & 31;
+  const int G = p.Hq / p.Hkv;
+  const int wph = 4 / hpb;   // waves per head
+  const int qt_len = wph * 32;
+  const int nqt = (p.Sq + qt_len - 1) / qt_len;
+  const int nhg = p.Hq / hpb;
+  const int bid = blockIdx.x;
+  const int qt = nqt - 1 - bid / (p.B * nhg); // heavy (late) query tiles first
+  const int rest = bid % (p.B * nhg);
+  const int b = rest / nhg, hg = rest % nhg;
+  const int hq = hg * hpb + w / wph;
+  const int hk = (hg * hpb) / G;
+  const int q0 = qt * qt_len;
+  const int q_last = (q0 + qt_len < p.Sq ? q0 + qt_len : p.Sq) - 1;
+  const int qi = q0 + (w % wph) * 32 + ql;
+  const int off = p.Sk - p.Sq;
+
+  // key band of the whole block
+  int hi = p.Sk, lo = 0;
+  if (p.right >= 0) {
+    const int lim = q_last + off + p.right + 1;
+    hi = lim < hi ? lim : hi;
+  }
+  if (p.left >= 0) {
+    const int lim = q0 + off - p.left;
+    lo = lim > 0 ? lim : 0;
+  }
+  const int t_begin = lo / kKvTile;
+  const int t_end = hi > lo ? (hi + kKvTile - 1) / kKvTile : t_begin;
+
+  const T *qp = (const T *)p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh;
+  const T *kp = (const T *)p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  const T *vp = (const T *)p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
+
+  V8 zero;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) zero[i] = (T)0.0f;
+
+  V8 qf[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+    qf[ks] = qi < p.Sq ? *reinterpret_cast<const V8 *>(qp + (int64_t)qi * p.q_ss + ks * 16 + h * 8)
+                       : zero;
+
+  // staging registers for the next tile
+  constexpr int KCH = kKvTile * CPR / 256; // K chunks per thread (4 for D=128)
+  V8 rk[KCH];
+  V8 rv[4];
+  const bool vthread = tid < 16 * CPR;
+  const int vkg = tid / CPR, vch = tid % CPR;
+  auto gload = [&](int t) {
+    const int kb = t * kKvTile;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + 256 * i, key = c / CPR, ch = c % CPR;
+      const int kk = kb + key;
+      rk[i] = kk < p.Sk ? *reinterpret_cast<const V8 *>(kp + (int64_t)kk * p.k_ss + ch * 8) : zero;
+    }
+    if (vthread) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kk = kb + vkg * 4 + i;
+        rv[i] = kk < p.Sk ? *reinterpret_cast<const V8 *>(vp + (int64_t)kk * p.v_ss + vch * 8)
+                          : zero;
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + 256 * i, key = c / CPR, ch = c % CPR;
+      sm.k[buf][key * CPR + (ch ^ (key & (CPR - 1)))] = rk[i];
+    }
+    if (vthread) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int d = vch * 8 + j;
+        const uint64_t e0 = __builtin_bit_cast(uint16_t, rv[0][j]);
+        const uint64_t e1 = __builtin_bit_cast(uint16_t, rv[1][j]);
+        const uint64_t e2 = __builtin_bit_cast(uint16_t, rv[2][j]);
+        const uint64_t e3 = __builtin_bit_cast(uint16_t, rv[3][j]);
+        sm.vt[buf][d * 16 + (vkg ^ vt_swz(d))] = e0 | (e1 << 16) | (e2 << 32) | (e3 << 48);
+      }
+    }
+  };
+
+  f32x16 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  if (t_begin < t_end) {
+    gload(t_begin);
+    sstore(0);
+  }
+  __syncthreads();
+  for (int t = t_begin; t < t_end; ++t) {
+    const int buf = (t - t_begin) & 1;
+    if (t + 1 < t_end) gload(t + 1);
+    const int kb = t * kKvTile;
+
+    f32x16 s[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[st][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const int key = st * 32 + ql, ch = ks * 2 + h;
+        const V8 a = sm.k[buf][key * CPR + (ch ^ (key & (CPR - 1)))];
+        s[st] = mfma32x32<T>(a, qf[ks], s[st]);
+      }
+    }
+    // scores -> log2 domain, masking on band edges only
+    const bool edge = (p.right >= 0 && kb + kKvTile - 1 > q0 + off + p.right) ||
+                      (p.left >= 0 && kb < q_last + off - p.left) || (kb + kKvTile > p.Sk);
+    float mt = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[st][r] * p.scale_log2;
+        if (edge) {
+          const int j = kb + st * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+          const int rel = j - (qi + off);
+          bool keep = j < p.Sk;
+          if (p.right >= 0) keep = keep && rel <= p.right;
+          if (p.left >= 0) keep = keep && rel >= -p.left;
+          x = keep ? x : -INFINITY;
+        }
+        s[st][r] = x;
+        mt = fmaxf(mt, x);
+      }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const float m_new = fmaxf(m_run, mt);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    float psum = 0.f;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float e = exp2f(s[st][r] - m_use);
+        s[st][r] = e;
+        psum += e;
+      }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[tt][r] *= alpha;
+
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int st = c >> 1, c2 = c & 1;
+      V8 pb;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pb[j] = from_f32<T>(s[st][c2 * 8 + j]);
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) {
+        const int d = tt * 32 + ql;
+        const int sw = vt_swz(d);
+        const uint64_t u0 = sm.vt[buf][d * 16 + ((4 * c + h) ^ sw)];
+        const uint64_t u1 = sm.vt[buf][d * 16 + ((4 * c + 2 + h) ^ sw)];
+        u32x4 raw = {(uint32_t)u0, (uint32_t)(u0 >> 32), (uint32_t)u1, (uint32_t)(u1 >> 32)};
+        const V8 a = __builtin_bit_cast(V8, raw);
+        o[tt] = mfma32x32<T>(a, pb, o[tt]);
+      }
+    }
+    if (t + 1 < t_end) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  const float l = l_run + __shfl_xor(l_run, 32, kWave);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (qi >= p.Sq) return;
+  T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)qi * p.o_ss + (int64_t)hq * p.o_sh;
+  typedef typename VecT<T>::v4 V4;
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      V4 pk;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pk[i] = from_f32<T>(o[tt][rg * 4 + i] * inv);
+      *reinterpret_cast<V4 *>(op + tt * 32 + rg * 8 + h * 4) = pk;
+    }
+}
+
+// Generic prefill (any D <= 256, any alignment): one wave per (b, query,
+// head), keys streamed one at a time with a wave reduction. Slow; exists so
+// that every head size flash-attn accepts still runs on the GPU.
+template <typename T>
+__global__ __launch_bounds__(64) void attn_generic_kernel(AttnArgs p, int D) {
+  const int lane = threadIdx.x;
+  const int64_t id = blockIdx.x; // (b, qi, hq)
+  const int hq = (int)(id % p.Hq);
+  const int qi = (int)((id / p.Hq) % p.Sq);
+  const int b = (int)(id / ((int64_t)p.Hq * p.Sq));
+  const int hk = hq / (p.Hq / p.Hkv);
+  const int off = p.Sk - p.Sq;
+  const T *qp = (const T *)p.q + b * p.q_sb + (int64_t)qi * p.q_ss + hq * p.q_sh;
+  const T *kp = (const T *)p.k + b * p.k_sb + hk * p.k_sh;
+  const T *vp = (const T *)p.v + b * p.v_sb + hk * p.v_sh;
+  float qv[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane + 64 * i;
+    qv[i] = d < D ? to_f32(qp[d]) * p.scale_log2 : 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  for (int j = 0; j < p.Sk; ++j) {
+    const int rel = j - (qi + off);
+    if (p.right >= 0 && rel > p.right) break;
+    if (p.left >= 0 && rel < -p.left) continue;
+    float sdot = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = lane + 64 * i;
+      if (d < D) sdot += qv[i] * to_f32(kp[(int64_t)j * p.k_ss + d]);
+    }
+    sdot = wave_sum(sdot);
+    const float mn = fmaxf(m, sdot);
+    const float a = exp2f(m - mn), e = exp2f(sdot - mn);
+    l = l * a + e;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = lane + 64 * i;
+      acc[i] = acc[i] * a + (d < D ? e * to_f32(vp[(int64_t)j * p.v_ss + d]) : 0.f);
+    }
+    m = mn;
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T *op = (T *)p.o + b * p.o_sb + (int64_t)qi * p.o_ss + hq * p.o_sh;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane + 64 * i;
+    if (d < D) op[d] = from_f32<T>(acc[i] * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode: one query per sequence against keys [lo_b, L_b) of the cache.
+// grid = (nsplit, Hkv, B), block = 256 (4 waves); G = Hq / Hkv <= 8.
+// ---------------------------------------------------------------------------
+constexpr int kDecMaxG = 8;
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int *__restrict__ seqlens,
+                                                          int fixed_len, float *__restrict__ ws_o,
+                                                          float *__restrict__ ws_ml, int chunk,
+                                                          int nsplit) {
+  typedef typename VecT<T>::v8 V8;
+  constexpr int LPK = D / 8;        // lanes per key
+  constexpr int KPW = kWave / LPK;  // keys per wave pass
+  constexpr int U = 4;              // passes per load batch
+  __shared__ float red_m[4][G], red_l[4][G];
+  __shared__ float red_o[4][G][D];
+
+  const int lane = lane_id(), w = wave_id();
+  const int row = lane / LPK, dp = lane % LPK;
+  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  int L = seqlens ? seqlens[b] : fixed_len;
+  L = L < p.Sk ? (L > 0 ? L : 0) : p.Sk; // never read past the cache
+  int lo = 0;
+  if (p.left >= 0) lo = L - 1 - p.left > 0 ? L - 1 - p.left : 0;
+  int k_begin = split * chunk, k_end = k_begin + chunk;
+  k_begin = k_begin > lo ? k_begin : lo;
+  k_end = k_end < L ? k_end : L;
+
+  float qv[G][8];
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    const T *qp = (const T *)p.q + (int64_t)b * p.q_sb + (int64_t)(hk * G + gi) * p.q_sh + dp * 8;
+    load8(qp, qv[gi]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qv[gi][j] *= p.scale_log2;
+  }
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    m[gi] = -INFINITY;
+    l[gi] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[gi][j] = 0.f;
+  }
+  const T *kp = (const T *)p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + dp * 8;
+  const T *vp = (const T *)p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh + dp * 8;
+  V8 zero;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) zero[i] = (T)0.0f;
+
+  for (int base = k_begin + w * KPW; base < k_end; base += 4 * KPW * U) {
+    V8 kr[U], vr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key = base + u * 4 * KPW + row;
+      const bool ok = key < k_end;
+      kr[u] = ok ? *reinterpret_cast<const V8 *>(kp + (int64_t)key * p.k_ss) : zero;
+      vr[u] = ok ? *reinterpret_cast<const V8 *>(vp + (int64_t)key * p.v_ss) : zero;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key = base + u * 4 * KPW + row;
+      const bool ok = key < k_end;
+      float kf[8], vf[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        kf[j] = to_f32(kr[u][j]);
+        vf[j] = to_f32(vr[u][j]);
+      }
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        float sdot = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sdot += qv[gi][j] * kf[j];
+        sdot += dpp_f32<kDppQuadXor1>(sdot);
+        sdot += dpp_f32<kDppQuadXor2>(sdot);
+        if constexpr (LPK >= 8) sdot += dpp_f32<kDppRowHalfMirror>(sdot);
+        if constexpr (LPK >= 16) sdot += dpp_f32<kDppRowMirror>(sdot);
+        if (ok) {
+          const float mn = fmaxf(m[gi], sdot);
+          const float a = exp2f(m[gi] - mn), e = exp2f(sdot - mn);
+          l[gi] = l[gi] * a + e;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[gi][j] = acc[gi][j] * a + e * vf[j];
+          m[gi] = mn;
+        }
+      }
+    }
+  }
+  // merge the KPW key rows of the wave (lanes with equal dp)
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+#pragma unroll
+    for (int sh = LPK; sh < kWave; sh <<= 1) {
+      const float mo = __shfl_xor(m[gi], sh, kWave);
+      const float lo2 = __shfl_xor(l[gi], sh, kWave);
+      const float mn = fmaxf(m[gi], mo);
+      const float mu = mn == -INFINITY ? 0.f : mn;
+      const float a = exp2f(m[gi] - mu), c = exp2f(mo - mu);
+      l[gi] = l[gi] * a + lo2 * c;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float ao = __shfl_xor(acc[gi][j], sh, kWave);
+        acc[gi][j] = acc[gi][j] * a + ao * c;
+      }
+      m[gi] = mn;
+    }
+    if (row == 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) red_o[w][gi][dp * 8 + j] = acc[gi][j];
+      if (dp == 0) {
+        red_m[w][gi] = m[gi];
+        red_l[w][gi] = l[gi];
+      }
+    }
+  }
+  __syncthreads();
+  // merge the 4 waves: thread -> (gi, d)
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int gi = idx / D, d = idx % D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) mx = fmaxf(mx, red_m[ww][gi]);
+    const float mu = mx == -INFINITY ? 0.f : mx;
+    float ls = 0.f, os = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float c = exp2f(red_m[ww][gi] - mu);
+      ls += red_l[ww][gi] * c;
+      os += red_o[ww][gi][d] * c;
+    }
+    const int hq = hk * G + gi;
+    const int64_t slot = ((int64_t)b * p.Hq + hq) * nsplit + split;
+    ws_o[slot * D + d] = os;
+    if (d == 0) {
+      ws_ml[slot * 2] = mx;
+      ws_ml[slot * 2 + 1] = ls;
+    }
+  }
+}
+
+// Combine the chunk partials: grid (Hq, B), one wave.
+template <typename T>
+__global__ __launch_bounds__(64) void attn_decode_combine_kernel(AttnArgs p, int D,
+                                                                 const float *__restrict__ ws_o,
+                                                                 const float *__restrict__ ws_ml,
+                                                                 int nsplit) {
+  const int hq = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int64_t s0 = ((int64_t)b * p.Hq + hq) * nsplit;
+  float mx = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ws_ml[(s0 + s) * 2]);
+  const float mu = mx == -INFINITY ? 0.f : mx;
+  float ls = 0.f;
+  for (int s = 0; s < nsplit; ++s) ls += ws_ml[(s0 + s) * 2 + 1] * exp2f(ws_ml[(s0 + s) * 2] - mu);
+  const float inv = ls > 0.f ? 1.f / ls : 0.f;
+  T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
+  for (int d = lane; d < D; d += 64) {
+    float os = 0.f;
+    for (int s = 0; s < nsplit; ++s) os += ws_o[(s0 + s) * D + d] * exp2f(ws_ml[(s0 + s) * 2] - mu);
+    op[d] = from_f32<T>(os * inv);
+  }
+}
+
+static int check_attn(const char *name, const AttnArgs &a, int64_t D) {
+  if (!a.q || !a.k || !a.v || !a.o) return set_error(TPP_E_INVALID, "%s: null pointer", name);
+  if (a.B < 0 || a.Sq < 0 || a.Sk < 0 || a.Hq <= 0 || a.Hkv <= 0 || D <= 0)
+    return set_error(TPP_E_INVALID, "%s: invalid shapes", name);
+  if (a.Hq % a.Hkv != 0)
+    return set_error(TPP_E_INVALID, "%s: Hq (%d) must be a multiple of Hkv (%d)", name, a.Hq,
+                     a.Hkv);
+  if (D > 256) return set_error(TPP_E_UNSUPPORTED, "%s: head_dim %lld > 256", name, (long long)D);
+  return TPP_OK;
+}
+
+static bool strides16(const AttnArgs &a) {
+  auto al = [](int64_t s) { return s % 8 == 0; };
+  return aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) && al(a.q_sb) &&
+         al(a.q_ss) && al(a.q_sh) && al(a.k_sb) && al(a.k_ss) && al(a.k_sh) && al(a.v_sb) &&
+         al(a.v_ss) && al(a.v_sh) && al(a.o_sb) && al(a.o_ss) && al(a.o_sh);
+}
+
+template <typename T>
+static int launch_prefill(const AttnArgs &a, int64_t D, hipStream_t st, const char *name) {
+  if (a.B == 0 || a.Sq == 0) return TPP_OK;
+  const int G = a.Hq / a.Hkv;
+  if ((D == 64 || D == 128) && strides16(a)) {
+    const int hpb = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
+    const int qt_len = (4 / hpb) * 32;
+    const int64_t blocks =
+        (int64_t)a.B * (a.Hq / hpb) * ((a.Sq + qt_len - 1) / qt_len);
+    if (blocks > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: too large", name);
+    if (D == 128)
+      attn_prefill_kernel<T, 128><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a, hpb);
+    else
+      attn_prefill_kernel<T, 64><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a, hpb);
+  } else {
+    const int64_t blocks = (int64_t)a.B * a.Sq * a.Hq;
+    if (blocks > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: too large", name);
+    attn_generic_kernel<T><<<dim3((unsigned)blocks), dim3(64), 0, st>>>(a, (int)D);
+  }
+  return check_launch(name);
+}
+
+struct DecodePlan {
+  int chunk, nsplit;
+  size_t ws_bytes;
+};
+
+static DecodePlan plan_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t Lmax) {
+  DecodePlan pl{};
+  const int64_t groups = B * Hkv > 0 ? B * Hkv : 1;
+  int64_t want = (1024 + groups - 1) / groups; // ~1024 blocks
+  if (want < 1) want = 1;
+  int64_t chunk = (Lmax + want - 1) / want;
+  chunk = ((chunk + 63) / 64) * 64;
+  if (chunk < 64) chunk = 64;
+  if (chunk > 2048) chunk = 2048;
+  pl.chunk = (int)chunk;
+  pl.nsplit = (int)((Lmax + chunk - 1) / chunk);
+  if (pl.nsplit < 1) pl.nsplit = 1;
+  pl.ws_bytes = (size_t)(B * Hq * pl.nsplit) * (size_t)(D + 2) * sizeof(float);
+  return pl;
+}
+
+template <typename T, int D, int G>
+static void launch_decode_g(const AttnArgs &a, dim3 grid, const int *seqlens, int L, float *ws_o,
+                            float *ws_ml, const DecodePlan &pl, hipStream_t st) {
+  attn_decode_kernel<T, D, G><<<grid, dim3(256), 0, st>>>(a, seqlens, L, ws_o, ws_ml, pl.chunk,
+                                                         pl.nsplit);
+}
+
+template <typename T, int D>
+static void launch_decode_d(const AttnArgs &a, int G, dim3 grid, const int *seqlens, int L,
+                            float *ws_o, float *ws_ml, const DecodePlan &pl, hipStream_t st) {
+  switch (G) {
+  case 1: launch_decode_g<T, D, 1>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
+  case 2: launch_decode_g<T, D, 2>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
+  case 3: launch_decode_g<T, D, 3>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
+  case 4: launch_decode_g<T, D, 4>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
+  case 5: launch_decode_g<T, D, 5>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
+  case 6: launch_decode_g<T, D, 6>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
+  case 7: launch_decode_g<T, D, 7>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
+  default: launch_decode_g<T, D, 8>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
+  }
+}
+
+template <typename T>
+static void launch_decode(const AttnArgs &a, int64_t D, int G, dim3 grid, const int *seqlens,
+                          int L, float *ws_o, float *ws_ml, const DecodePlan &pl, hipStream_t st) {
+  if (D == 128) launch_decode_d<T, 128>(a, G, grid, seqlens, L, ws_o, ws_ml, pl, st);
+  else launch_decode_d<T, 64>(a, G, grid, seqlens, L, ws_o, ws_ml, pl, st);
+}
+
+} // namespace tpp
+
+using namespace tpp;
+
+static AttnArgs make_args(const void *q, const void *k, const void *v, void *o,
+                          const int64_t *qs, const int64_t *ks, const int64_t *vs,
+                          const int64_t *os, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq,
+                          int64_t Hkv, int64_t D, float scale, int left, int right) {
+  AttnArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.q_sb = qs[0], a.q_ss = qs[1], a.q_sh = qs[2];
+  a.k_sb = ks[0], a.k_ss = ks[1], a.k_sh = ks[2];
+  a.v_sb = vs[0], a.v_ss = vs[1], a.v_sh = vs[2];
+  a.o_sb = os[0], a.o_ss = os[1], a.o_sh = os[2];
+  a.B = (int)B, a.Sq = (int)Sq, a.Sk = (int)Sk, a.Hq = (int)Hq, a.Hkv = (int)Hkv;
+  const float sc = scale > 0.f ? scale : 1.0f / sqrtf((float)D);
+  a.scale_log2 = sc * kLog2e;
+  a.left = left;
+  a.right = right;
+  return a;
+}
+
+extern "C" int tpp_attn_prefill(const void *q, const void *k, const void *v, void *o,
+                                const int64_t *q_strides, const int64_t *k_strides,
+                                const int64_t *v_strides, const int64_t *o_strides, int64_t B,
+                                int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D,
+                                float softmax_scale, int causal, int window_left,
+                                int window_right, int dtype, void *stream) {
+  const char *name = "tpp_attn_prefill";
+  if (!q_strides || !k_strides || !v_strides || !o_strides)
+    return set_error(TPP_E_INVALID, "%s: null stride array", name);
+  if (B > 0x7fffffff || Sq > 0x7fffffff || Sk > 0x7fffffff)
+    return set_error(TPP_E_UNSUPPORTED, "%s: dimension too large", name);
+  const int right = causal ? 0 : (window_right < 0 ? -1 : window_right);
+  const int left = window_left < 0 ? -1 : window_left;
+  AttnArgs a = make_args(q, k, v, o, q_strides, k_strides, v_strides, o_strides, B, Sq, Sk, Hq,
+                         Hkv, D, softmax_scale, left, right);
+  if (int e = check_attn(name, a, D)) return e;
+  hipStream_t st = as_stream(stream);
+  return TPP_DISPATCH_HALF(dtype, [&] { return launch_prefill<T>(a, D, st, name); });
+}
+
+extern "C" size_t tpp_attn_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                                 int64_t Lmax) {
+  return plan_decode(B, Hq, Hkv, D, Lmax).ws_bytes;
+}
+
+extern "C" int tpp_attn_decode(const void *q, const void *k_cache, const void *v_cache, void *o,
+                               const int64_t *q_strides, const int64_t *k_strides,
+                               const int64_t *v_strides, const int64_t *o_strides,
+                               const int32_t *seqlens, int64_t B, int64_t Hq, int64_t Hkv,
+                               int64_t D, int64_t Lmax, float softmax_scale, int window_left,
+                               int dtype, void *workspace, size_t ws_bytes, void *stream) {
+  const char *name = "tpp_attn_decode";
+  if (!q_strides || !k_strides || !v_strides || !o_strides)
+    return set_error(TPP_E_INVALID, "%s: null stride array", name);
+  if (B > 0xffff || Hkv > 0xffff || Lmax > 0x7fffffff)
+    return set_error(TPP_E_UNSUPPORTED, "%s: dimension too large", name);
+  AttnArgs a = make_args(q, k_cache, v_cache, o, q_strides, k_strides, v_strides, o_strides, B,
+                         1, Lmax, Hq, Hkv, D, softmax_scale, window_left < 0 ? -1 : window_left,
+                         0);
+  if (int e = check_attn(name, a, D)) return e;
+  if (B == 0) return TPP_OK;
+  if (D != 64 && D != 128)
+    return set_error(TPP_E_UNSUPPORTED, "%s: head_dim %lld not in {64, 128}", name, (long long)D);
+  if (Hq / Hkv > kDecMaxG)
+    return set_error(TPP_E_UNSUPPORTED, "%s: more than %d query heads per KV head", name,
+                     kDecMaxG);
+  if (!strides16(a)) return set_error(TPP_E_INVALID, "%s: 16-byte alignment required", name);
+  const DecodePlan pl = plan_decode(B, Hq, Hkv, D, Lmax);
+  if (!workspace || ws_bytes < pl.ws_bytes || !aligned16(workspace))
+    return set_error(TPP_E_WORKSPACE, "%s: workspace of %zu bytes required", name, pl.ws_bytes);
+  float *ws_o = (float *)workspace;
+  float *ws_ml = ws_o + (size_t)(B * Hq * pl.nsplit) * D;
+  hipStream_t st = as_stream(stream);
+  const dim3 grid((unsigned)pl.nsplit, (unsigned)Hkv, (unsigned)B);
+  return TPP_DISPATCH_HALF(dtype, [&] {
+    launch_decode<T>(a, D, (int)(Hq / Hkv), grid, seqlens, (int)Lmax, ws_o, ws_ml, pl, st);
+    if (int e = check_launch(name)) return e;
+    attn_decode_combine_kernel<T><<<dim3((unsigned)Hq, (unsigned)B), dim3(64), 0, st>>>(
+        a, (int)D, ws_o, ws_ml, pl.nsplit);
+    return check_launch(name);
+  });
+}

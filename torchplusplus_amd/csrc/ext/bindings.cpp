@@ -388,9 +388,114 @@ at::Tensor gemv_swiglu(at::Tensor input, at::Tensor w_gu) {
   return out;
 }
 
+// ---- attention (flash_attn_func contract) ----------------------------------
+void check_bshd(const at::Tensor &t, const char *what) {
+  TORCH_CHECK(t.is_cuda(), what, " must be on CUDA");
+  TORCH_CHECK(is_half_or_bf16(t), what, " must be float16 or bfloat16");
+  TORCH_CHECK(t.dim() == 4, what, " must be 4D [batch, seqlen, heads, head_dim]");
+  TORCH_CHECK(t.stride(3) == 1, what, " must have a contiguous last dimension");
+}
+
+at::Tensor attn_fwd(at::Tensor q, at::Tensor k, at::Tensor v, bool causal, int64_t window_left,
+                    int64_t window_right, double softmax_scale) {
+  check_bshd(q, "q");
+  check_bshd(k, "k");
+  check_bshd(v, "v");
+  TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(),
+              "q, k, v must share a dtype");
+  const int64_t B = q.size(0), Sq = q.size(1), Hq = q.size(2), D = q.size(3);
+  const int64_t Sk = k.size(1), Hkv = k.size(2);
+  TORCH_CHECK(k.size(0) == B && v.size(0) == B, "batch size mismatch");
+  TORCH_CHECK(k.size(3) == D && v.size(3) == D, "head_dim mismatch");
+  TORCH_CHECK(v.size(1) == Sk && v.size(2) == Hkv, "k and v shapes differ");
+  TORCH_CHECK(Hq % Hkv == 0, "number of query heads must be divisible by KV heads");
+  c10::DeviceGuard g(q.device());
+  auto o = torch::empty({B, Sq, Hq, D}, q.options());
+  const int64_t qs[3] = {q.stride(0), q.stride(1), q.stride(2)};
+  const int64_t ks[3] = {k.stride(0), k.stride(1), k.stride(2)};
+  const int64_t vs[3] = {v.stride(0), v.stride(1), v.stride(2)};
+  const int64_t os[3] = {o.stride(0), o.stride(1), o.stride(2)};
+  check_rc(tpp_attn_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), qs, ks, vs,
+                            os, B, Sq, Sk, Hq, Hkv, D, (float)softmax_scale, causal ? 1 : 0,
+                            (int)window_left, (int)window_right, dtype_code(q), cur_stream(q)),
+           "flash_attn_func");
+  return o;
+}
+
+// q [B, 1, Hq, D]; caches [B, Hkv, Lmax, D] (strides honoured); seqlens int32 [B]
+at::Tensor attn_decode(at::Tensor q, at::Tensor k_cache, at::Tensor v_cache,
+                       c10::optional<at::Tensor> seqlens, double softmax_scale,
+                       int64_t window_left, c10::optional<at::Tensor> out) {
+  check_bshd(q, "q");
+  TORCH_CHECK(q.size(1) == 1, "decode expects one query per sequence");
+  TORCH_CHECK(k_cache.is_cuda() && v_cache.is_cuda() && k_cache.dim() == 4 &&
+                  k_cache.sizes() == v_cache.sizes() && k_cache.stride(3) == 1 &&
+                  v_cache.stride(3) == 1,
+              "caches must be CUDA [B, Hkv, Lmax, D] with a contiguous last dim");
+  TORCH_CHECK(k_cache.scalar_type() == q.scalar_type() &&
+                  v_cache.scalar_type() == q.scalar_type(),
+              "cache dtype must match q");
+  const int64_t B = q.size(0), Hq = q.size(2), D = q.size(3);
+  const int64_t Hkv = k_cache.size(1), Lmax = k_cache.size(2);
+  TORCH_CHECK(k_cache.size(0) == B && k_cache.size(3) == D, "cache shape mismatch");
+  const int32_t *sl = nullptr;
+  if (seqlens.has_value() && seqlens->defined()) {
+    TORCH_CHECK(seqlens->is_cuda() && seqlens->scalar_type() == at::kInt &&
+                    seqlens->numel() == B && seqlens->is_contiguous(),
+                "seqlens must be a contiguous CUDA int32 tensor [B]");
+    sl = seqlens->data_ptr<int32_t>();
+  }
+  c10::DeviceGuard g(q.device());
+  at::Tensor o;
+  if (out.has_value() && out->defined()) {
+    o = *out;
+    TORCH_CHECK(o.sizes() == q.sizes() && o.scalar_type() == q.scalar_type() &&
+                    o.stride(3) == 1,
+                "out must match q");
+  } else {
+    o = torch::empty_like(q);
+  }
+  const size_t wsb = tpp_attn_decode_workspace_size(B, Hq, Hkv, D, Lmax);
+  auto ws = torch::empty({(int64_t)((wsb + 3) / 4)}, q.options().dtype(at::kFloat));
+  const int64_t qs[3] = {q.stride(0), q.stride(1), q.stride(2)};
+  const int64_t ks[3] = {k_cache.stride(0), k_cache.stride(2), k_cache.stride(1)};
+  const int64_t vs[3] = {v_cache.stride(0), v_cache.stride(2), v_cache.stride(1)};
+  const int64_t os[3] = {o.stride(0), o.stride(1), o.stride(2)};
+  check_rc(tpp_attn_decode(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), o.data_ptr(),
+                           qs, ks, vs, os, sl, B, Hq, Hkv, D, Lmax, (float)softmax_scale,
+                           (int)window_left, dtype_code(q), ws.data_ptr(), wsb, cur_stream(q)),
+           "attn_decode");
+  return o;
+}
+
+at::Tensor argmax_rows(at::Tensor x) {
+  TORCH_CHECK(x.is_cuda() && is_half_or_bf16(x), "x must be a CUDA half/bfloat16 tensor");
+  TORCH_CHECK(x.stride(-1) == 1, "x must have a contiguous last dim");
+  const int64_t N = x.size(-1);
+  at::Tensor x2 = x.reshape({-1, N});
+  TORCH_CHECK(x2.stride(1) == 1, "x must be viewable as rows");
+  c10::DeviceGuard g(x.device());
+  auto out = torch::empty({x2.size(0)}, x.options().dtype(at::kLong));
+  check_rc(tpp_argmax_rows(x2.data_ptr(), out.data_ptr<int64_t>(), x2.size(0), N, x2.stride(0),
+                           dtype_code(x), cur_stream(x)),
+           "argmax_rows");
+  auto shp = x.sizes().vec();
+  shp.pop_back();
+  return out.view(shp);
+}
+
 } // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("argmax_rows", &argmax_rows, "argmax over the last dim (greedy sampling)", py::arg("x"));
+  m.def("flash_attn_func", &attn_fwd, "flash attention forward (GQA, causal, window)",
+        py::arg("q"), py::arg("k"), py::arg("v"), py::arg("causal") = false,
+        py::arg("window_left") = -1, py::arg("window_right") = -1,
+        py::arg("softmax_scale") = 0.0);
+  m.def("attn_decode", &attn_decode, "split-KV decode attention over a KV cache", py::arg("q"),
+        py::arg("k_cache"), py::arg("v_cache"), py::arg("seqlens") = py::none(),
+        py::arg("softmax_scale") = 0.0, py::arg("window_left") = -1,
+        py::arg("out") = py::none());
   m.def("rope_apply_cuda", &rope_apply_cuda, "RoPE (rotate-half), out of place",
         py::arg("x"), py::arg("cos_cache"), py::arg("sin_cache"));
   m.def("rope_apply_", &rope_apply_inplace, "RoPE (rotate-half), in place", py::arg("x"),

@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
         x2[j] = to_f32(from_f32<T>((x2[j] * inv) * w2[j]));
       }
     }
-    const int pr = p < ctx ? p : ctx - 1;
+    const int pr = p < 0 ? 0 : (p < ctx ? p : ctx - 1);
     float c1[8], c2[8], s1[8], s2[8];
     load_cs8(cos + (int64_t)pr * D + i0, c1);
     load_cs8(cos + (int64_t)pr * D + D / 2 + i0, c2);
@@ -232,7 +232,7 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
   } else {
     const int hk = is_k ? head - Hq : head - Hq - Hkv;
     T *cache = is_k ? k_cache : v_cache;
-    if (p >= Lmax) return; // host checks bounds; never write past the cache
+    if (p < 0 || p >= Lmax) return; // host checks bounds; never write outside the cache
     dst = cache + (((int64_t)b * Hkv + hk) * Lmax + p) * D;
   }
   store8(dst + i0, x1);

@@ -142,7 +142,7 @@ template <int ACT> __device__ __forceinline__ float apply_act(float x) {
 // ---- host-side error state -------------------------------------------------
 int set_error(int code, const char *fmt, ...);
 int check_launch(const char *what);
-inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+__host__ __device__ inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 inline int elem_size(int dtype) { return dtype == TPP_F32 ? 4 : 2; }
 inline bool half_type(int dtype) { return dtype == TPP_F16 || dtype == TPP_BF16; }
