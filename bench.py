@@ -1,0 +1,259 @@
+"""Benchmark: Qwen3-0.6B-shape greedy decode on one MI355X.
+
+Workload: random-init Qwen3-0.6B-architecture
+decoder (28 layers, hidden 1024, 16/8 heads, head_dim 128, SwiGLU 3072,
+vocab 151936, bf16, weights ~N(0, 0.02)), batch 8, prefill 2048 random token
+ids, then greedy decode. A step is one decode token for all 8 sequences (one
+replay of the captured decode graph); `value` = 8 * steps / time of the K
+timed steps at cache positions 2048..2048+K-1.
+
+Also printed in the same JSON line:
+  roofline      the dominant decode kernel (split-KV attention, HBM-bound):
+                algorithmic bytes per launch / average launch time measured
+                with HIP events on the stream it runs on
+  kernels       every decode/prefill kernel at its model shape, same method
+  prefill       time and tok/s of the 2048 x 8 prefill
+  cpu_baseline  the CPU oracle (PyTorch restatement of the reference model)
+                decoding on this host's cores, bounded sample
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
+METRIC = "Qwen3-0.6B-shape decode tok/s; per-kernel HBM GB/s & MFMA % of MI355X peak"
+BATCH, PREFILL = 8, 2048
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def event_time_us(fn, iters: int) -> float:
+    """Average GPU time of fn() over `iters` back-to-back calls (the queue stays
+    full, so the events bracket kernel execution, not host overhead)."""
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) * 1e3 / iters
+
+
+def hbm_entry(name, us, nbytes):
+    gbs = nbytes / us / 1e3
+    return {"kernel": name, "us": round(us, 3), "bound": "hbm", "bytes": int(nbytes),
+            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def mfma_entry(name, us, flops):
+    tf = flops / us / 1e6
+    return {"kernel": name, "us": round(us, 3), "bound": "mfma", "flops": int(flops),
+            "TFLOP/s": round(tf, 1), "frac": round(tf / MFMA_PEAK_TFLOPS, 4)}
+
+
+def measure_kernels(model, dec, cfg, L):
+    """Per-kernel timings at the decode (cache length L) and prefill shapes.
+    Each launch cycles over the 28 layers' weights / caches, so the bytes come
+    from HBM (2.1 GB of caches, 1.2 GB of weights >> the 256 MB MALL)."""
+    from torchplusplus_amd._native import ext
+
+    C = ext()
+    B, E, H, Hkv, D, I, V = BATCH, cfg.embed_dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.hidden_dim, cfg.vocab_size
+    dev = model.out_head.weight.device
+    dt = cfg.dtype
+    blocks = model.transformer_blocs
+    caches = model.kv_cache_array
+    nl = len(blocks)
+    g = torch.Generator(device=dev).manual_seed(1)
+    x1 = torch.randn(B, 1, E, generator=g, device=dev).to(dt)
+    out = []
+    it = {"i": 0}
+
+    def cyc():
+        it["i"] = (it["i"] + 1) % nl
+        return it["i"]
+
+    # decode attention at cache length L
+    q = torch.randn(B, 1, H, D, generator=g, device=dev).to(dt)
+    seq = torch.full((B,), L, dtype=torch.int32, device=dev)
+    o = torch.empty_like(q)
+
+    def attn():
+        c = caches[cyc()]
+        C.attn_decode(q, c.k_cache, c.v_cache, seq, 0.0, -1, o)
+
+    us = event_time_us(attn, 4 * nl)
+    attn_bytes = 2 * B * Hkv * L * D * 2 + 2 * B * H * D * 2
+    out.append(hbm_entry("attn_decode_kernel (+combine) B8 16/8 d128 L%d" % L, us, attn_bytes))
+    attn_us = us
+
+    def gemv_entry(name, wget, n, k, xin, fn=None):
+        def run():
+            w = wget(blocks[cyc()])
+            (fn or (lambda a, b: C.gemv(a, b, None, 0)))(xin, w)
+        t = event_time_us(run, 4 * nl)
+        out.append(hbm_entry(name, t, (n * k + B * k + B * n) * 2))
+
+    gemv_entry("gemv qkv [8x1024]x[4096x1024]^T", lambda b: b.attn.fused_qkv_weight(), 4096, E, x1)
+    xo = torch.randn(B, 1, H * D, generator=g, device=dev).to(dt)
+    gemv_entry("gemv o_proj [8x2048]x[1024x2048]^T", lambda b: b.attn.out_projection.weight, E, H * D, xo)
+    gemv_entry("gemv_swiglu gate/up [8x1024]x[6144x1024]^T", lambda b: b.ffn.w_gu(), 2 * I, E, x1,
+               lambda a, b: C.gemv_swiglu(a, b))
+    xd = torch.randn(B, 1, I, generator=g, device=dev).to(dt)
+    gemv_entry("gemv down [8x3072]x[1024x3072]^T", lambda b: b.ffn.linear_layer2.weight, E, I, xd)
+    wout = model.out_head.weight
+    t = event_time_us(lambda: C.gemv(x1, wout, None, 0), 8)
+    out.append(hbm_entry("gemv lm_head [8x1024]x[151936x1024]^T", t, (V * E + B * E + B * V) * 2))
+    # small per-token kernels (their bytes fit in the MALL: warm figures)
+    r = torch.randn(B, 1, E, generator=g, device=dev).to(dt)
+    w = blocks[0].rms_norm1.weight
+    t = event_time_us(lambda: C.add_rmsnorm(x1, r, w, 1e-6), 64)
+    out.append(hbm_entry("add_rmsnorm [8x1024] (warm)", t, 4 * B * E * 2 + E * 2))
+    # prefill shapes (MFMA-bound)
+    M = BATCH * PREFILL
+    xp = torch.randn(M, E, generator=g, device=dev).to(dt)
+    t = event_time_us(lambda: C.linear(xp, blocks[cyc()].attn.fused_qkv_weight(), None, 0), 2 * nl)
+    out.append(mfma_entry("gemm qkv [16384x1024]x[4096x1024]^T", t, 2 * M * 4096 * E))
+    t = event_time_us(lambda: C.linear_swiglu(xp, blocks[cyc()].ffn.w_gu()), 2 * nl)
+    out.append(mfma_entry("gemm swiglu [16384x1024]x[6144x1024]^T", t, 2 * M * 2 * I * E))
+    qp = torch.randn(BATCH, PREFILL, H, D, generator=g, device=dev).to(dt)
+    kp = torch.randn(BATCH, PREFILL, Hkv, D, generator=g, device=dev).to(dt)
+    t = event_time_us(lambda: C.flash_attn_func(qp, kp, kp, True, -1, -1, 0.0), 10)
+    keys = PREFILL * (PREFILL + 1) // 2
+    out.append(mfma_entry("attn_prefill causal B8 S2048 16/8 d128", t, 4 * BATCH * H * D * keys))
+    del xp, qp, kp
+    return out, attn_us, attn_bytes
+
+
+def cpu_baseline(model, cfg, steps: int = 3):
+    """The oracle's eager PyTorch decode (fp32 math, bf16 rounding at op
+    boundaries) on this host: batch 8, synthetic 2048-position cache."""
+    from oracle.qwen3 import Qwen3Oracle
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    orc = Qwen3Oracle(model.state_dict(), cfg, PREFILL + steps + 2)
+    g = torch.Generator().manual_seed(2)
+    orc.seed_cache(BATCH, PREFILL, g)
+    ids = torch.randint(0, cfg.vocab_size, (BATCH, 1), generator=g)
+    orc.forward(ids, PREFILL)  # warm-up step
+    t0 = time.perf_counter()
+    for s in range(steps):
+        logits = orc.forward(ids, PREFILL + 1 + s)
+        ids = logits[:, -1].argmax(-1, keepdim=True)
+    dt = time.perf_counter() - t0
+    return {"value": round(BATCH * steps / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{steps} greedy decode steps, batch {BATCH}, cache {PREFILL} positions "
+                      f"(random K/V), after 1 warm-up step; oracle/qwen3.py on the host CPU"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the decode path shards by KV head "
+              "across GPUs by design, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from torchplusplus_amd.fastqwen3 import FastQwen3, GreedyDecoder, QwenConfig
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = QwenConfig(dtype=torch.bfloat16)
+    K, W = args.steps, args.warmup
+    lmax = PREFILL + max(K, W) + 1
+    log(f"[bench] building model (28 layers, bf16), kv cache {lmax} positions")
+    with torch.inference_mode():
+        model = FastQwen3(cfg, device=dev, rope_context=lmax + 1).eval()
+        model.init_weights(std=0.02, generator=torch.Generator(device=dev).manual_seed(0))
+        ids = torch.randint(0, cfg.vocab_size, (BATCH, PREFILL),
+                            generator=torch.Generator().manual_seed(0)).to(dev)
+        model.setup_kv_cache(lmax, BATCH)
+
+        # prefill (timed separately; warm once)
+        model.reset_kv_cache()
+        model.forward_impl(ids, model.kv_cache_array, 0, last_only=True)
+        torch.cuda.synchronize()
+        model.reset_kv_cache()
+        t0 = time.perf_counter()
+        logits = model.forward_impl(ids, model.kv_cache_array, 0, last_only=True)
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        log(f"[bench] prefill {prefill_s * 1e3:.2f} ms")
+        first = torch.argmax(logits[:, -1], dim=-1)
+
+        dec = GreedyDecoder(model, BATCH)
+        dec.prepare(first, PREFILL)
+        dec.capture()
+        for _ in range(W):
+            dec.replay()
+        torch.cuda.synchronize()
+        dec.prepare(first, PREFILL)  # timed steps decode positions 2048..2048+K-1
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(K):
+            dec.replay()
+        torch.cuda.synchronize()
+        decode_s = time.perf_counter() - t0
+        log(f"[bench] decode {K} steps {decode_s * 1e3:.2f} ms")
+        tok_s = BATCH * K / decode_s
+
+        L = PREFILL + K // 2  # mean cache length over the timed steps
+        kernels, attn_us, attn_bytes = measure_kernels(model, dec, cfg, L)
+        log("[bench] kernel table done")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        cpu = cpu_baseline(model, cfg, args.cpu_steps)
+
+    achieved = attn_bytes / attn_us / 1e3
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(decode_s * 1e3 / K, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights ~N(0,0.02), random token ids",
+        "config": {"workload": "Qwen3-0.6B-shape greedy decode (28 layers, hidden 1024, 16/8 heads, "
+                               "head_dim 128, SwiGLU 3072, vocab 151936), batch 8, prefill 2048",
+                   "global_batch": BATCH, "prefill_len": PREFILL, "decode_steps": K,
+                   "parallelism": "single GPU"},
+        "roofline": {"kernel": "attn_decode_kernel", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": attn_bytes, "avg_launch_us": round(attn_us, 3),
+                     "cache_len": L},
+        "prefill": {"ms": round(prefill_s * 1e3, 3), "tok_per_s": round(BATCH * PREFILL / prefill_s, 1)},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

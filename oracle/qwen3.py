@@ -73,3 +73,12 @@ class Qwen3Oracle:
             x = _r(x + f, self.dt)
         h = self._norm(x, "final_rmsnorm.weight")
         return h @ self.w["out_head.weight"].t()
+
+    def seed_cache(self, batch: int, length: int, generator: torch.Generator):
+        """Fill every layer's K/V with `length` random positions (synthetic
+        decode context: a decode step costs the same whatever the values)."""
+        c = self.cfg
+        shape = (batch, length, c.n_kv_heads, c.head_dim)
+        for i in range(c.n_layers):
+            self.k[i] = torch.randn(shape, generator=generator).to(self.dt)
+            self.v[i] = torch.randn(shape, generator=generator).to(self.dt)

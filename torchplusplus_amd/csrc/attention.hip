@@ -151,14 +151,18 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs p, int hpb) 
       sm.k[buf][key * CPR + (ch ^ (key & (CPR - 1)))] = rk[i];
     }
     if (vthread) {
+      // Whole-vector bit casts: hipcc (clang 22) miscompiles a bit cast of a
+      // single __bf16 ext-vector element into a read of element 0.
+      const u16x8 w0 = __builtin_bit_cast(u16x8, rv[0]);
+      const u16x8 w1 = __builtin_bit_cast(u16x8, rv[1]);
+      const u16x8 w2 = __builtin_bit_cast(u16x8, rv[2]);
+      const u16x8 w3 = __builtin_bit_cast(u16x8, rv[3]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int d = vch * 8 + j;
-        const uint64_t e0 = __builtin_bit_cast(uint16_t, rv[0][j]);
-        const uint64_t e1 = __builtin_bit_cast(uint16_t, rv[1][j]);
-        const uint64_t e2 = __builtin_bit_cast(uint16_t, rv[2][j]);
-        const uint64_t e3 = __builtin_bit_cast(uint16_t, rv[3][j]);
-        sm.vt[buf][d * 16 + (vkg ^ vt_swz(d))] = e0 | (e1 << 16) | (e2 << 32) | (e3 << 48);
+        sm.vt[buf][d * 16 + (vkg ^ vt_swz(d))] = (uint64_t)w0[j] | ((uint64_t)w1[j] << 16) |
+                                                 ((uint64_t)w2[j] << 32) |
+                                                 ((uint64_t)w3[j] << 48);
       }
     }
   };
