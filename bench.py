@@ -39,18 +39,30 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def event_time_us(fn, iters: int) -> float:
-    """Average GPU time of fn() over `iters` back-to-back calls (the queue stays
-    full, so the events bracket kernel execution, not host overhead)."""
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    fn()
+def event_time_us(fn, iters: int, reps: int = 5) -> float:
+    """Average GPU time per call of fn(): `iters` calls are captured into one
+    HIP graph (so back-to-back kernels are timed, not Python launch
+    overhead), the graph is replayed `reps` times between HIP events recorded
+    on the stream the kernels run on (torch's current stream)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm-up: allocations and lazily built fused weights
+    torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    s.record()
-    for _ in range(iters):
-        fn()
-    e.record()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) * 1e3 / iters
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for _ in range(reps):
+        graph.replay()
+    en.record()
+    torch.cuda.synchronize()
+    return st.elapsed_time(en) * 1e3 / (reps * iters)
 
 
 def hbm_entry(name, us, nbytes):
@@ -96,7 +108,7 @@ def measure_kernels(model, dec, cfg, L):
         c = caches[cyc()]
         C.attn_decode(q, c.k_cache, c.v_cache, seq, 0.0, -1, o)
 
-    us = event_time_us(attn, 4 * nl)
+    us = event_time_us(attn, nl)
     attn_bytes = 2 * B * Hkv * L * D * 2 + 2 * B * H * D * 2
     out.append(hbm_entry("attn_decode_kernel (+combine) B8 16/8 d128 L%d" % L, us, attn_bytes))
     attn_us = us
@@ -105,34 +117,49 @@ def measure_kernels(model, dec, cfg, L):
         def run():
             w = wget(blocks[cyc()])
             (fn or (lambda a, b: C.gemv(a, b, None, 0)))(xin, w)
-        t = event_time_us(run, 4 * nl)
+        t = event_time_us(run, nl)
         out.append(hbm_entry(name, t, (n * k + B * k + B * n) * 2))
 
-    gemv_entry("gemv qkv [8x1024]x[4096x1024]^T", lambda b: b.attn.fused_qkv_weight(), 4096, E, x1)
+    nw = blocks[0].rms_norm1.weight
+    gemv_entry("gemv qkv +rmsnorm [8x1024]x[4096x1024]^T", lambda b: b.attn.fused_qkv_weight(), 4096, E,
+               x1, lambda a, b: C.gemv_fused(a, b, nw, 1e-6))
     xo = torch.randn(B, 1, H * D, generator=g, device=dev).to(dt)
-    gemv_entry("gemv o_proj [8x2048]x[1024x2048]^T", lambda b: b.attn.out_projection.weight, E, H * D, xo)
-    gemv_entry("gemv_swiglu gate/up [8x1024]x[6144x1024]^T", lambda b: b.ffn.w_gu(), 2 * I, E, x1,
-               lambda a, b: C.gemv_swiglu(a, b))
+    res = torch.randn(B, 1, E, generator=g, device=dev).to(dt)
+    gemv_entry("gemv o_proj +residual [8x2048]x[1024x2048]^T", lambda b: b.attn.out_projection.weight,
+               E, H * D, xo, lambda a, b: C.gemv_fused(a, b, None, 1e-6, res))
+    gemv_entry("gemv_swiglu gate/up +rmsnorm [8x1024]x[6144x1024]^T", lambda b: b.ffn.w_gu(), 2 * I, E,
+               x1, lambda a, b: C.gemv_swiglu(a, b, nw, 1e-6))
     xd = torch.randn(B, 1, I, generator=g, device=dev).to(dt)
-    gemv_entry("gemv down [8x3072]x[1024x3072]^T", lambda b: b.ffn.linear_layer2.weight, E, I, xd)
+    gemv_entry("gemv down +residual [8x3072]x[1024x3072]^T", lambda b: b.ffn.linear_layer2.weight, E, I,
+               xd, lambda a, b: C.gemv_fused(a, b, None, 1e-6, res))
     wout = model.out_head.weight
-    t = event_time_us(lambda: C.gemv(x1, wout, None, 0), 8)
-    out.append(hbm_entry("gemv lm_head [8x1024]x[151936x1024]^T", t, (V * E + B * E + B * V) * 2))
-    # small per-token kernels (their bytes fit in the MALL: warm figures)
-    r = torch.randn(B, 1, E, generator=g, device=dev).to(dt)
-    w = blocks[0].rms_norm1.weight
-    t = event_time_us(lambda: C.add_rmsnorm(x1, r, w, 1e-6), 64)
-    out.append(hbm_entry("add_rmsnorm [8x1024] (warm)", t, 4 * B * E * 2 + E * 2))
+    fw = model.final_rmsnorm.weight
+    t = event_time_us(lambda: C.gemv_argmax(x1, wout, fw, 1e-6, False), 8)
+    out.append(hbm_entry("gemv_argmax lm_head +rmsnorm [8x1024]x[151936x1024]^T (+partials)", t,
+                         (V * E + B * E) * 2))
+    # per-token QK-norm + RoPE + KV append (bytes fit in the MALL: warm figure)
+    qkv = torch.randn(B, 1, (H + 2 * Hkv) * D, generator=g, device=dev).to(dt)
+    qo = torch.empty(B, 1, H, D, dtype=dt, device=dev)
+    pos = torch.full((B,), L, dtype=torch.int32, device=dev)
+    a0 = blocks[0].attn
+
+    def rope():
+        c = caches[cyc()]
+        C.qkv_rope_cache(qkv, qo, c.k_cache, c.v_cache, a0.q_norm.weight, a0.k_norm.weight,
+                         model.cos, model.sin, pos, 1e-6)
+
+    t = event_time_us(rope, 2 * nl)
+    out.append(hbm_entry("qkv_rope_cache [8 tokens, 16+8+8 heads]", t, 2 * B * (H + 2 * Hkv) * D * 2 + 4 * B * 2 * D * 2))
     # prefill shapes (MFMA-bound)
     M = BATCH * PREFILL
     xp = torch.randn(M, E, generator=g, device=dev).to(dt)
-    t = event_time_us(lambda: C.linear(xp, blocks[cyc()].attn.fused_qkv_weight(), None, 0), 2 * nl)
+    t = event_time_us(lambda: C.linear(xp, blocks[cyc()].attn.fused_qkv_weight(), None, 0), nl)
     out.append(mfma_entry("gemm qkv [16384x1024]x[4096x1024]^T", t, 2 * M * 4096 * E))
-    t = event_time_us(lambda: C.linear_swiglu(xp, blocks[cyc()].ffn.w_gu()), 2 * nl)
+    t = event_time_us(lambda: C.linear_swiglu(xp, blocks[cyc()].ffn.w_gu()), nl)
     out.append(mfma_entry("gemm swiglu [16384x1024]x[6144x1024]^T", t, 2 * M * 2 * I * E))
     qp = torch.randn(BATCH, PREFILL, H, D, generator=g, device=dev).to(dt)
     kp = torch.randn(BATCH, PREFILL, Hkv, D, generator=g, device=dev).to(dt)
-    t = event_time_us(lambda: C.flash_attn_func(qp, kp, kp, True, -1, -1, 0.0), 10)
+    t = event_time_us(lambda: C.flash_attn_func(qp, kp, kp, True, -1, -1, 0.0), 4)
     keys = PREFILL * (PREFILL + 1) // 2
     out.append(mfma_entry("attn_prefill causal B8 S2048 16/8 d128", t, 4 * BATCH * H * D * keys))
     del xp, qp, kp

@@ -148,26 +148,37 @@ int tpp_linear_swiglu(const void *x, const void *w_gu, void *y, int64_t M,
                       int64_t I, int64_t K, int64_t ldx, int64_t ldy,
                       int dtype, void *stream);
 
-/* Bytes of zero-initialised workspace tpp_gemv / tpp_gemv_swiglu need for
- * batch B, N weight rows (2I for swiglu) and K (0 = none). */
-size_t tpp_gemv_workspace_size(int64_t B, int64_t N, int64_t K, int swiglu);
-
 /* Decode GEMV, y[B, N] = act(T(x[B, K] . W[N, K]^T + bias)), B <= 16,
- * streaming W once for all B rows. workspace: see tpp_gemv_workspace_size; it
- * must be zero when first used and is left zero by every call, so it can be
- * reused without clearing; calls sharing it must be stream-ordered.
+ * streaming W once for all B rows (MFMA 16x16x32 tiles of 16 weight rows, K
+ * split across the waves of a block). bias may be NULL, act a tpp_act.
  * Replaces hgemvK128F16x4Kernel / launchHgemv
  * (csrc/blas/hgemv/hgemv_kernels.cuh:19-85), which had no binding. */
 int tpp_gemv(const void *x, const void *W, const void *bias, void *y,
              int64_t B, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
-             int act, int dtype, void *workspace, size_t ws_bytes,
-             void *stream);
+             int act, int dtype, void *stream);
 
-/* Decode SwiGLU GEMV over an interleaved w_gu [2I, K] (layout as in
- * tpp_linear_swiglu): y[B, I]. */
-int tpp_gemv_swiglu(const void *x, const void *W_gu, void *y, int64_t B,
-                    int64_t I, int64_t K, int64_t ldx, int64_t ldy, int dtype,
-                    void *workspace, size_t ws_bytes, void *stream);
+/* Decode GEMV with the decoder-block fusions (x, y, residual contiguous):
+ *   norm_w != NULL : the input is RMSNorm(x) * norm_w with eps (the
+ *                    RmsNormFused before each projection, fastqwen3.py:108,114)
+ *   residual != NULL: residual[B, N] <- T(residual + T(x W^T)) in place, y
+ *                    unused (the residual adds of fastqwen3.py:111,116)
+ *   swiglu != 0     : W is the interleaved [gate|up] weight of
+ *                    tpp_linear_swiglu (N = 2I rows) and y is [B, I]. */
+int tpp_gemv_fused(const void *x, const void *norm_w, float eps, const void *W,
+                   void *y, void *residual, int64_t B, int64_t N, int64_t K,
+                   int swiglu, int dtype, void *stream);
+
+/* Workspace bytes of tpp_gemv_argmax (no initialisation required). */
+size_t tpp_gemv_argmax_workspace_size(int64_t B, int64_t N);
+
+/* lm_head + greedy sampling: logits = RMSNorm(x)*norm_w . W^T (norm_w may be
+ * NULL; logits may be NULL), out_idx[b] = argmax_n logits[b, n] (first index
+ * of the maximum of the T-rounded logits), replacing out_head + sample_greedy
+ * (fastqwen3.py:187-188, torchpp/llmops/llm.py:181-186). */
+int tpp_gemv_argmax(const void *x, const void *norm_w, float eps,
+                    const void *W, void *logits, int64_t *out_idx, int64_t B,
+                    int64_t N, int64_t K, int dtype, void *workspace,
+                    size_t ws_bytes, void *stream);
 
 /* ---- attention ----------------------------------------------------------- */
 
@@ -189,7 +200,8 @@ int tpp_attn_prefill(const void *q, const void *k, const void *v, void *o,
                      int window_left, int window_right, int dtype,
                      void *stream);
 
-/* Bytes of workspace tpp_attn_decode needs (no initialisation required). */
+/* Bytes of workspace tpp_attn_decode needs (no initialisation required;
+ * calls that share a workspace must be ordered, e.g. on one stream). */
 size_t tpp_attn_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv,
                                       int64_t D, int64_t Lmax);
 

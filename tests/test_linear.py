@@ -75,8 +75,8 @@ def test_gemv_parity(dev, dtype, bsz, n, k):
     close(y, oracle.gemv(x, w), what=f"gemv b{bsz} {n}x{k}")
 
 
-def test_gemv_repeated_calls_keep_workspace_clean(dev):
-    """The split-K workspace is self-cleaning: many calls in a row, same result."""
+def test_gemv_repeated_calls_are_deterministic(dev):
+    """No cross-block reduction: repeated calls give bit-identical results."""
     x, w, _ = _mk(8, 1024, 3072, torch.bfloat16, seed=6)
     xd, wd = x.to(dev), w.to(dev)
     first = ext().gemv(xd, wd)
@@ -109,3 +109,56 @@ def test_swiglu_gemm_and_gemv(dev, rows):
     gt = oracle.linear_act(x, wg)
     e = (torch.nn.functional.silu(gt.float()).bfloat16().float() * oracle.linear_act(x, wu).float()).bfloat16()
     close(y, e, what=f"swiglu rows={rows}")
+
+
+@pytest.mark.parametrize("bsz", [1, 8])
+@pytest.mark.parametrize("n,k", [(4096, 1024), (1024, 3072), (40, 1024)])
+def test_gemv_fused_input_rmsnorm(dev, bsz, n, k):
+    x, w, _ = _mk(bsz, n, k, torch.bfloat16, seed=9)
+    nw = (1 + 0.1 * torch.randn(k, generator=torch.Generator().manual_seed(10))).bfloat16()
+    y = ext().gemv_fused(x.to(dev), w.to(dev), nw.to(dev), 1e-6)
+    close(y, oracle.linear_act(oracle.rmsnorm(x, nw, 1e-6), w), what="gemv(rmsnorm(x))")
+
+
+@pytest.mark.parametrize("n,k", [(1024, 2048), (1024, 3072)])
+def test_gemv_fused_residual_add(dev, n, k):
+    x, w, _ = _mk(8, n, k, torch.bfloat16, seed=11)
+    r = torch.randn(8, n, generator=torch.Generator().manual_seed(12)).bfloat16()
+    rd = r.to(dev)
+    out = ext().gemv_fused(x.to(dev), w.to(dev), None, 1e-6, rd)
+    assert out.data_ptr() == rd.data_ptr()
+    e = (r.float() + oracle.linear_act(x, w).float()).bfloat16()
+    close(rd, e, what="residual += x W^T")
+
+
+def test_gemv_swiglu_with_input_norm(dev):
+    g = torch.Generator().manual_seed(13)
+    I, K = 3072, 1024
+    x = torch.randn(8, K, generator=g).bfloat16()
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).bfloat16()
+    wg = (0.02 * torch.randn(I, K, generator=g)).bfloat16()
+    wu = (0.02 * torch.randn(I, K, generator=g)).bfloat16()
+    y = ext().gemv_swiglu(x.to(dev), L.interleave_gate_up(wg, wu).to(dev), nw.to(dev), 1e-6)
+    h = oracle.rmsnorm(x, nw, 1e-6)
+    gt = oracle.linear_act(h, wg)
+    e = (torch.nn.functional.silu(gt.float()).bfloat16().float() * oracle.linear_act(h, wu).float()).bfloat16()
+    close(y, e, what="swiglu(rmsnorm(x))")
+
+
+@pytest.mark.parametrize("bsz,n", [(8, 151936), (3, 1000), (1, 17)])
+def test_gemv_argmax_lm_head(dev, bsz, n):
+    x, w, _ = _mk(bsz, n, 1024, torch.bfloat16, seed=14)
+    nw = (1 + 0.1 * torch.randn(1024, generator=torch.Generator().manual_seed(15))).bfloat16()
+    idx, logits = ext().gemv_argmax(x.to(dev), w.to(dev), nw.to(dev), 1e-6, True)
+    assert torch.equal(idx.cpu(), torch.argmax(logits.cpu().float(), dim=-1))
+    close(logits, oracle.linear_act(oracle.rmsnorm(x, nw, 1e-6), w), what="lm_head logits")
+    only = ext().gemv_argmax(x.to(dev), w.to(dev), nw.to(dev), 1e-6, False)
+    assert len(only) == 1 and torch.equal(only[0], idx)
+
+
+def test_argmax_first_index_on_ties(dev):
+    x = torch.zeros(2, 1000).bfloat16()
+    x[0, [5, 700]] = 3.0
+    x[1, 999] = 1.0
+    x[1, 998] = 1.0
+    assert ext().argmax_rows(x.to(dev)).cpu().tolist() == [5, 998]

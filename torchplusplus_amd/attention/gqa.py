@@ -61,28 +61,29 @@ class GroupedQueryAttention(nn.Module):
             self.refresh_fused_weights()
         return self._wqkv
 
-    def project_rope_cache(self, x, cos, sin, k_dst, v_dst, positions):
-        """Steps 1-2: returns q [B, S, Hq, D]; K/V rows land in k_dst/v_dst
-        ([B, Hkv, L, D]) at positions[b] + s."""
-        bs, seq_len, _ = x.shape
-        qkv = linear(x, self.fused_qkv_weight())
-        q = torch.empty(bs, seq_len, self.num_heads, self.head_dim, dtype=x.dtype, device=x.device)
-        eps = self.q_norm.eps if self.q_norm is not None else 1e-6
+    def rope_cache(self, qkv, cos, sin, k_dst, v_dst, positions):
+        """Step 2 on a projected qkv [B, S, (Hq+2Hkv)*D]: returns q [B, S, Hq, D];
+        K/V rows land in k_dst/v_dst ([B, Hkv, L, D]) at positions[b] + s."""
+        bs, seq_len = qkv.shape[0], qkv.shape[1]
+        q = torch.empty(bs, seq_len, self.num_heads, self.head_dim, dtype=qkv.dtype, device=qkv.device)
+        eps = self.q_norm.eps if self.q_norm is not None and self.q_norm.eps is not None else 1e-6
         _C.qkv_rope_cache(qkv, q, k_dst, v_dst,
                           self.q_norm.weight if self.q_norm is not None else None,
                           self.k_norm.weight if self.k_norm is not None else None,
-                          cos, sin, positions, eps if eps is not None else 1e-6)
+                          cos, sin, positions, eps)
         return q
 
-    def forward(self, x, cos, sin, kv_cache: Optional[KVCache] = None,
-                cache_pos: Optional[int] = None):
-        bs, seq_len, _ = x.shape
-        dev = x.device
+    def attend(self, qkv, cos, sin, kv_cache: Optional[KVCache] = None,
+               cache_pos: Optional[int] = None) -> torch.Tensor:
+        """Steps 2-3: rope/cache the projected qkv and attend; returns the
+        attention output [B, S, Hq*D] (before the output projection)."""
+        bs, seq_len = qkv.shape[0], qkv.shape[1]
+        dev = qkv.device
         if kv_cache is not None:
             start = kv_cache.cache_len if cache_pos is None else int(cache_pos)
             kv_cache.ensure(bs, start + seq_len)
             positions = torch.full((bs,), start, dtype=torch.int32, device=dev)
-            q = self.project_rope_cache(x, cos, sin, kv_cache.k_cache, kv_cache.v_cache, positions)
+            q = self.rope_cache(qkv, cos, sin, kv_cache.k_cache, kv_cache.v_cache, positions)
             kv_cache.cache_len = max(kv_cache.cache_len, start + seq_len)
             total = start + seq_len
             if seq_len == 1:
@@ -93,9 +94,14 @@ class GroupedQueryAttention(nn.Module):
                 vc = kv_cache.v_cache[:bs, :, :total].transpose(1, 2)
                 o = flash_attn_func(q, kc, vc, causal=True)
         else:
-            k = torch.empty(bs, self.n_kv_heads, seq_len, self.head_dim, dtype=x.dtype, device=dev)
+            k = torch.empty(bs, self.n_kv_heads, seq_len, self.head_dim, dtype=qkv.dtype, device=dev)
             v = torch.empty_like(k)
             positions = torch.zeros(bs, dtype=torch.int32, device=dev)
-            q = self.project_rope_cache(x, cos, sin, k, v, positions)
+            q = self.rope_cache(qkv, cos, sin, k, v, positions)
             o = flash_attn_func(q, k.transpose(1, 2), v.transpose(1, 2), causal=True)
-        return linear(o.reshape(bs, seq_len, self.d_out), self.out_projection.weight)
+        return o.reshape(bs, seq_len, self.d_out)
+
+    def forward(self, x, cos, sin, kv_cache: Optional[KVCache] = None,
+                cache_pos: Optional[int] = None):
+        qkv = linear(x, self.fused_qkv_weight())
+        return linear(self.attend(qkv, cos, sin, kv_cache, cache_pos), self.out_projection.weight)

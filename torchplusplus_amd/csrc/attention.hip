@@ -32,7 +32,7 @@
 // Decode kernel: a block = (batch, KV head, key chunk); each 16-lane DPP row
 // (D/8 lanes) handles one key, all query heads of the group are scored
 // against it, online softmax per lane, then log-sum-exp merges across rows,
-// waves (LDS) and chunks (a second small kernel).
+// waves (LDS) and chunks (a small merge kernel per (batch, KV head)).
 #include "tpp_common.hpp"
 
 namespace tpp {
@@ -331,8 +331,14 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(AttnArgs p, int D) {
 // ---------------------------------------------------------------------------
 // Decode: one query per sequence against keys [lo_b, L_b) of the cache.
 // grid = (nsplit, Hkv, B), block = 256 (4 waves); G = Hq / Hkv <= 8.
+// A wave takes KPW keys per pass (one per D/8-lane DPP row) and issues the
+// K and V loads of kDecU passes before using any of them; the online
+// softmax is updated once per batch of passes.
 // ---------------------------------------------------------------------------
 constexpr int kDecMaxG = 8;
+constexpr int kDecU = 8;
+
+constexpr int kDecMaxSplit = 256;
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int *__restrict__ seqlens,
@@ -342,7 +348,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int 
   typedef typename VecT<T>::v8 V8;
   constexpr int LPK = D / 8;        // lanes per key
   constexpr int KPW = kWave / LPK;  // keys per wave pass
-  constexpr int U = 4;              // passes per load batch
+  constexpr int U = kDecU;
   __shared__ float red_m[4][G], red_l[4][G];
   __shared__ float red_o[4][G][D];
 
@@ -388,16 +394,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int 
       kr[u] = ok ? *reinterpret_cast<const V8 *>(kp + (int64_t)key * p.k_ss) : zero;
       vr[u] = ok ? *reinterpret_cast<const V8 *>(vp + (int64_t)key * p.v_ss) : zero;
     }
+    float sc[U][G];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int key = base + u * 4 * KPW + row;
-      const bool ok = key < k_end;
-      float kf[8], vf[8];
+      const bool ok = base + u * 4 * KPW + row < k_end;
+      float kf[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        kf[j] = to_f32(kr[u][j]);
-        vf[j] = to_f32(vr[u][j]);
-      }
+      for (int j = 0; j < 8; ++j) kf[j] = to_f32(kr[u][j]);
 #pragma unroll
       for (int gi = 0; gi < G; ++gi) {
         float sdot = 0.f;
@@ -407,15 +410,27 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int 
         sdot += dpp_f32<kDppQuadXor2>(sdot);
         if constexpr (LPK >= 8) sdot += dpp_f32<kDppRowHalfMirror>(sdot);
         if constexpr (LPK >= 16) sdot += dpp_f32<kDppRowMirror>(sdot);
-        if (ok) {
-          const float mn = fmaxf(m[gi], sdot);
-          const float a = exp2f(m[gi] - mn), e = exp2f(sdot - mn);
-          l[gi] = l[gi] * a + e;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[gi][j] = acc[gi][j] * a + e * vf[j];
-          m[gi] = mn;
-        }
+        sc[u][gi] = ok ? sdot : -INFINITY;
       }
+    }
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      float mb = m[gi];
+#pragma unroll
+      for (int u = 0; u < U; ++u) mb = fmaxf(mb, sc[u][gi]);
+      const float mu = mb == -INFINITY ? 0.f : mb;
+      const float alpha = exp2f(m[gi] - mu);
+      l[gi] *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[gi][j] *= alpha;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float e = exp2f(sc[u][gi] - mu);
+        l[gi] += e;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[gi][j] += e * to_f32(vr[u][j]);
+      }
+      m[gi] = mb;
     }
   }
   // merge the KPW key rows of the wave (lanes with equal dp)
@@ -446,7 +461,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int 
     }
   }
   __syncthreads();
-  // merge the 4 waves: thread -> (gi, d)
+  // merge the 4 waves: thread -> (gi, d); write this chunk's partial
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int gi = idx / D, d = idx % D;
     float mx = -INFINITY;
@@ -470,25 +485,50 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int 
   }
 }
 
-// Combine the chunk partials: grid (Hq, B), one wave.
-template <typename T>
-__global__ __launch_bounds__(64) void attn_decode_combine_kernel(AttnArgs p, int D,
-                                                                 const float *__restrict__ ws_o,
-                                                                 const float *__restrict__ ws_ml,
-                                                                 int nsplit) {
-  const int hq = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const int64_t s0 = ((int64_t)b * p.Hq + hq) * nsplit;
-  float mx = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ws_ml[(s0 + s) * 2]);
-  const float mu = mx == -INFINITY ? 0.f : mx;
-  float ls = 0.f;
-  for (int s = 0; s < nsplit; ++s) ls += ws_ml[(s0 + s) * 2 + 1] * exp2f(ws_ml[(s0 + s) * 2] - mu);
-  const float inv = ls > 0.f ? 1.f / ls : 0.f;
-  T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
-  for (int d = lane; d < D; d += 64) {
+// Merge the chunk partials of one (batch, KV head): grid (Hkv, B), 256
+// threads, G query heads. A separate launch on purpose: publishing partials
+// across blocks inside one kernel needs device-scope release/acquire fences,
+// which on MI355X write back / invalidate the XCD's L2 (the 8 XCD L2s are not
+// coherent) and cost far more than a kernel boundary.
+template <typename T, int D, int G>
+__global__ __launch_bounds__(256) void attn_decode_merge_kernel(AttnArgs p,
+                                                                const float *__restrict__ ws_o,
+                                                                const float *__restrict__ ws_ml,
+                                                                int nsplit) {
+  __shared__ float s_w[G][kDecMaxSplit], s_l[G][kDecMaxSplit], s_inv[G];
+  const int hk = blockIdx.x, b = blockIdx.y, lane = lane_id(), w = wave_id();
+  const int64_t s0 = ((int64_t)b * p.Hq + hk * G) * nsplit; // slot of (gi = 0, split 0)
+  for (int idx = threadIdx.x; idx < G * nsplit; idx += blockDim.x) {
+    const int gi = idx / nsplit, sp = idx % nsplit;
+    const float *ml = ws_ml + (s0 + (int64_t)gi * nsplit + sp) * 2;
+    s_w[gi][sp] = ml[0];
+    s_l[gi][sp] = ml[1];
+  }
+  __syncthreads();
+  for (int gi = w; gi < G; gi += 4) { // one wave per query head
+    float mx = -INFINITY;
+    for (int sp = lane; sp < nsplit; sp += kWave) mx = fmaxf(mx, s_w[gi][sp]);
+#pragma unroll
+    for (int sh = 1; sh < kWave; sh <<= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, kWave));
+    const float mu = mx == -INFINITY ? 0.f : mx;
+    float ls = 0.f;
+    for (int sp = lane; sp < nsplit; sp += kWave) {
+      const float wgt = exp2f(s_w[gi][sp] - mu);
+      s_w[gi][sp] = wgt;
+      ls += wgt * s_l[gi][sp];
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) s_inv[gi] = ls > 0.f ? 1.f / ls : 0.f;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int gi = idx / D, d = idx % D;
+    const float *po = ws_o + (s0 + (int64_t)gi * nsplit) * D + d;
     float os = 0.f;
-    for (int s = 0; s < nsplit; ++s) os += ws_o[(s0 + s) * D + d] * exp2f(ws_ml[(s0 + s) * 2] - mu);
-    op[d] = from_f32<T>(os * inv);
+#pragma unroll 8
+    for (int sp = 0; sp < nsplit; ++sp) os += s_w[gi][sp] * po[(int64_t)sp * D];
+    T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)(hk * G + gi) * p.o_sh;
+    op[d] = from_f32<T>(os * s_inv[gi]);
   }
 }
 
@@ -539,13 +579,9 @@ struct DecodePlan {
 
 static DecodePlan plan_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t Lmax) {
   DecodePlan pl{};
-  const int64_t groups = B * Hkv > 0 ? B * Hkv : 1;
-  int64_t want = (1024 + groups - 1) / groups; // ~1024 blocks
-  if (want < 1) want = 1;
-  int64_t chunk = (Lmax + want - 1) / want;
-  chunk = ((chunk + 63) / 64) * 64;
-  if (chunk < 64) chunk = 64;
-  if (chunk > 2048) chunk = 2048;
+  const int64_t keys_per_batch = 4 * (kWave / (D / 8)) * kDecU; // one load batch per wave
+  int64_t chunk = keys_per_batch;
+  while ((Lmax + chunk - 1) / chunk > kDecMaxSplit) chunk += keys_per_batch;
   pl.chunk = (int)chunk;
   pl.nsplit = (int)((Lmax + chunk - 1) / chunk);
   if (pl.nsplit < 1) pl.nsplit = 1;
@@ -558,6 +594,8 @@ static void launch_decode_g(const AttnArgs &a, dim3 grid, const int *seqlens, in
                             float *ws_ml, const DecodePlan &pl, hipStream_t st) {
   attn_decode_kernel<T, D, G><<<grid, dim3(256), 0, st>>>(a, seqlens, L, ws_o, ws_ml, pl.chunk,
                                                          pl.nsplit);
+  attn_decode_merge_kernel<T, D, G><<<dim3(grid.y, grid.z), dim3(256), 0, st>>>(a, ws_o, ws_ml,
+                                                                               pl.nsplit);
 }
 
 template <typename T, int D>
@@ -663,9 +701,6 @@ extern "C" int tpp_attn_decode(const void *q, const void *k_cache, const void *v
   const dim3 grid((unsigned)pl.nsplit, (unsigned)Hkv, (unsigned)B);
   return TPP_DISPATCH_HALF(dtype, [&] {
     launch_decode<T>(a, D, (int)(Hq / Hkv), grid, seqlens, (int)Lmax, ws_o, ws_ml, pl, st);
-    if (int e = check_launch(name)) return e;
-    attn_decode_combine_kernel<T><<<dim3((unsigned)Hq, (unsigned)B), dim3(64), 0, st>>>(
-        a, (int)D, ws_o, ws_ml, pl.nsplit);
     return check_launch(name);
   });
 }

@@ -339,56 +339,112 @@ at::Tensor linear_swiglu(at::Tensor input, at::Tensor w_gu) {
   return out;
 }
 
-// Per-device zeroed GEMV workspace, reused (the kernels leave it zero).
-at::Tensor gemv_workspace(const at::Tensor &like, size_t bytes) {
-  // intentionally leaked: no tensor destructor runs after the allocator is gone
-  static std::vector<at::Tensor> *cache = new std::vector<at::Tensor>(64);
-  const int dev = like.device().index();
-  TORCH_CHECK(dev >= 0 && dev < 64, "device index out of range");
-  at::Tensor &ws = (*cache)[dev];
-  if (bytes == 0) bytes = 16;
-  if (!ws.defined() || (size_t)ws.numel() * 4 < bytes) {
-    size_t n = (bytes + 3) / 4;
-    n = n < (1u << 20) ? (1u << 20) : n; // at least 4 MiB
-    ws = torch::zeros({(int64_t)n}, like.options().dtype(at::kFloat));
-  }
-  return ws;
+void check_rows16(const at::Tensor &input, int64_t K) {
+  const int64_t B = input.numel() / K;
+  TORCH_CHECK(B >= 1 && B <= 16, "gemv supports 1..16 input rows, got ", B);
 }
 
 at::Tensor gemv(at::Tensor input, at::Tensor weight, c10::optional<at::Tensor> bias,
                 int64_t act) {
   check_linear(input, weight);
   const int64_t K = weight.size(1), N = weight.size(0), B = input.numel() / K;
-  TORCH_CHECK(B >= 1 && B <= 16, "gemv supports 1..16 input rows, got ", B);
+  check_rows16(input, K);
   const void *bp = bias_ptr(bias, input, N);
   c10::DeviceGuard g(input.device());
   auto out = torch::empty(out_shape(input, N), input.options());
-  const size_t wsb = tpp_gemv_workspace_size(B, N, K, 0);
-  at::Tensor ws = gemv_workspace(input, wsb);
   check_rc(tpp_gemv(input.data_ptr(), weight.data_ptr(), bp, out.data_ptr(), B, N, K, K, N,
-                    (int)act, dtype_code(input), ws.data_ptr(), (size_t)ws.numel() * 4,
-                    cur_stream(input)),
+                    (int)act, dtype_code(input), cur_stream(input)),
            "gemv");
   return out;
 }
 
-at::Tensor gemv_swiglu(at::Tensor input, at::Tensor w_gu) {
-  check_linear(input, w_gu);
-  const int64_t K = w_gu.size(1), I = w_gu.size(0) / 2, B = input.numel() / K;
-  TORCH_CHECK(B >= 1 && B <= 16, "gemv supports 1..16 input rows, got ", B);
-  TORCH_CHECK(w_gu.size(0) % 64 == 0, "w_gu rows must be a multiple of 64");
+const void *norm_ptr(const c10::optional<at::Tensor> &nw, const at::Tensor &input, int64_t K) {
+  if (!nw.has_value() || !nw->defined()) return nullptr;
+  TORCH_CHECK(nw->is_cuda() && nw->scalar_type() == input.scalar_type() &&
+                  nw->is_contiguous() && nw->numel() == K,
+              "norm weight must be a contiguous CUDA tensor [K] of the input dtype");
+  return nw->data_ptr();
+}
+
+// y = [norm](x) @ W^T, or residual += [norm](x) @ W^T (returns residual)
+at::Tensor gemv_fused(at::Tensor input, at::Tensor weight, c10::optional<at::Tensor> norm_w,
+                      double eps, c10::optional<at::Tensor> residual) {
+  check_linear(input, weight);
+  const int64_t K = weight.size(1), N = weight.size(0), B = input.numel() / K;
+  check_rows16(input, K);
+  const void *nw = norm_ptr(norm_w, input, K);
   c10::DeviceGuard g(input.device());
-  auto out = torch::empty(out_shape(input, I), input.options());
-  const size_t wsb = tpp_gemv_workspace_size(B, 2 * I, K, 1);
-  at::Tensor ws = gemv_workspace(input, wsb);
-  check_rc(tpp_gemv_swiglu(input.data_ptr(), w_gu.data_ptr(), out.data_ptr(), B, I, K, K, I,
-                           dtype_code(input), ws.data_ptr(), (size_t)ws.numel() * 4,
-                           cur_stream(input)),
+  if (residual.has_value() && residual->defined()) {
+    TORCH_CHECK(residual->is_cuda() && residual->is_contiguous() &&
+                    residual->scalar_type() == input.scalar_type() && residual->numel() == B * N,
+                "residual must be a contiguous [B, N] tensor of the input dtype");
+    check_rc(tpp_gemv_fused(input.data_ptr(), nw, (float)eps, weight.data_ptr(), nullptr,
+                            residual->data_ptr(), B, N, K, 0, dtype_code(input),
+                            cur_stream(input)),
+             "gemv_fused");
+    return *residual;
+  }
+  auto out = torch::empty(out_shape(input, N), input.options());
+  check_rc(tpp_gemv_fused(input.data_ptr(), nw, (float)eps, weight.data_ptr(), out.data_ptr(),
+                          nullptr, B, N, K, 0, dtype_code(input), cur_stream(input)),
+           "gemv_fused");
+  return out;
+}
+
+at::Tensor gemv_swiglu(at::Tensor input, at::Tensor w_gu, c10::optional<at::Tensor> norm_w,
+                       double eps) {
+  check_linear(input, w_gu);
+  const int64_t K = w_gu.size(1), N = w_gu.size(0), B = input.numel() / K;
+  check_rows16(input, K);
+  TORCH_CHECK(N % 64 == 0, "w_gu rows must be a multiple of 64");
+  const void *nw = norm_ptr(norm_w, input, K);
+  c10::DeviceGuard g(input.device());
+  auto out = torch::empty(out_shape(input, N / 2), input.options());
+  check_rc(tpp_gemv_fused(input.data_ptr(), nw, (float)eps, w_gu.data_ptr(), out.data_ptr(),
+                          nullptr, B, N, K, 1, dtype_code(input), cur_stream(input)),
            "gemv_swiglu");
   return out;
 }
 
+// greedy lm_head: returns (token ids [B] int64, logits or None)
+std::vector<at::Tensor> gemv_argmax(at::Tensor input, at::Tensor weight,
+                                    c10::optional<at::Tensor> norm_w, double eps,
+                                    bool return_logits) {
+  check_linear(input, weight);
+  const int64_t K = weight.size(1), N = weight.size(0), B = input.numel() / K;
+  check_rows16(input, K);
+  const void *nw = norm_ptr(norm_w, input, K);
+  c10::DeviceGuard g(input.device());
+  auto idx = torch::empty({B}, input.options().dtype(at::kLong));
+  at::Tensor logits;
+  if (return_logits) logits = torch::empty({B, N}, input.options());
+  const size_t wsb = tpp_gemv_argmax_workspace_size(B, N);
+  auto ws = torch::empty({(int64_t)((wsb + 3) / 4)}, input.options().dtype(at::kFloat));
+  check_rc(tpp_gemv_argmax(input.data_ptr(), nw, (float)eps, weight.data_ptr(),
+                           return_logits ? logits.data_ptr() : nullptr, idx.data_ptr<int64_t>(),
+                           B, N, K, dtype_code(input), ws.data_ptr(), wsb, cur_stream(input)),
+           "gemv_argmax");
+  if (return_logits) return {idx, logits};
+  return {idx};
+}
+
 // ---- attention (flash_attn_func contract) ----------------------------------
+// Per-device workspace for tpp_attn_decode, allocated once and reused, so a
+// captured decode graph keeps one stable pointer. Intentionally leaked: no
+// tensor destructor runs after the caching allocator is torn down at exit.
+at::Tensor cached_workspace(const at::Tensor &like, size_t bytes) {
+  static std::vector<at::Tensor> *cache = new std::vector<at::Tensor>(64);
+  const int dev = like.device().index();
+  TORCH_CHECK(dev >= 0 && dev < 64, "device index out of range");
+  at::Tensor &ws = (*cache)[dev];
+  if (!ws.defined() || (size_t)ws.numel() * 4 < bytes) {
+    int64_t n = (int64_t)((bytes + 3) / 4);
+    n = n < (1 << 20) ? (1 << 20) : n;
+    ws = torch::zeros({n}, like.options().dtype(at::kFloat));
+  }
+  return ws;
+}
+
 void check_bshd(const at::Tensor &t, const char *what) {
   TORCH_CHECK(t.is_cuda(), what, " must be on CUDA");
   TORCH_CHECK(is_half_or_bf16(t), what, " must be float16 or bfloat16");
@@ -456,7 +512,7 @@ at::Tensor attn_decode(at::Tensor q, at::Tensor k_cache, at::Tensor v_cache,
     o = torch::empty_like(q);
   }
   const size_t wsb = tpp_attn_decode_workspace_size(B, Hq, Hkv, D, Lmax);
-  auto ws = torch::empty({(int64_t)((wsb + 3) / 4)}, q.options().dtype(at::kFloat));
+  at::Tensor ws = cached_workspace(q, wsb);
   const int64_t qs[3] = {q.stride(0), q.stride(1), q.stride(2)};
   const int64_t ks[3] = {k_cache.stride(0), k_cache.stride(2), k_cache.stride(1)};
   const int64_t vs[3] = {v_cache.stride(0), v_cache.stride(2), v_cache.stride(1)};
@@ -520,7 +576,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gemv", &gemv, "decode GEMV for <= 16 rows", py::arg("input"), py::arg("weight"),
         py::arg("bias") = py::none(), py::arg("act") = 0);
   m.def("gemv_swiglu", &gemv_swiglu, "decode SwiGLU GEMV for <= 16 rows", py::arg("input"),
-        py::arg("w_gu"));
+        py::arg("w_gu"), py::arg("norm_weight") = py::none(), py::arg("eps") = 1e-6);
+  m.def("gemv_fused", &gemv_fused,
+        "decode GEMV with optional input RMSNorm and in-place residual add", py::arg("input"),
+        py::arg("weight"), py::arg("norm_weight") = py::none(), py::arg("eps") = 1e-6,
+        py::arg("residual") = py::none());
+  m.def("gemv_argmax", &gemv_argmax, "lm_head GEMV fused with greedy argmax", py::arg("input"),
+        py::arg("weight"), py::arg("norm_weight") = py::none(), py::arg("eps") = 1e-6,
+        py::arg("return_logits") = false);
   m.doc() = "torchpp gfx950 kernel set (binding over libtorchpp_hip.so)";
   m.def("rmsnormFused", &rmsnorm_fused, "Fused RMSNorm (fp16/bf16)", py::arg("input"),
         py::arg("weight"), py::arg("eps") = 1e-6);

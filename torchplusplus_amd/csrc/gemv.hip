@@ -5,33 +5,33 @@
 // hgemvCpu (hgemv_bench.cpp:10-24). In the model these GEMVs are the
 // nn.Linear calls of a decode step (B = batch size, one token each).
 //
-// Design (HBM-bound on W):
-//  * A wave owns a tile of 16 weight rows and a K slice. One
-//    v_mfma_f32_16x16x32 consumes 16 rows x 32 K of W (the B operand: each
-//    lane loads 16 contiguous bytes of one row) and the matching 16 x 32 of x
-//    (the A operand, batch rows >= B are zero). So the batch is free: W is
-//    streamed once for all B <= 16 rows of x, with 128-bit loads only.
-//  * The K range is split over the 4 waves of a block (LDS reduction) and,
-//    when there are too few row tiles to fill 256 CUs, over blocks: the
-//    partial sums go to an fp32 workspace with global float atomics and the
-//    last block of a row tile (device-scope counter) applies the epilogue,
-//    then zeroes its workspace slice and counter. The workspace therefore
-//    stays zero between calls (it must be zero when first used), which keeps
-//    the op free of memsets and safe to capture in a HIP graph. Calls that
-//    share one workspace must be ordered (same stream).
-//  * Epilogues: plain; bias + activation with the reference's rounding
-//    (pre-activation rounded to T, activation in fp32, csrc/activation/
-//    fused_gemm.cuh:93-105); SwiGLU over a [gate|up] weight interleaved in
-//    blocks of 32 rows (rows 64j..64j+31 = gate rows 32j.., the next 32 = up),
-//    rounding like the eager chain silu(gate(x)) * up(x).
+// Design (HBM-bound on W, latency-bound at decode sizes):
+//  * A block owns 16 weight rows. One v_mfma_f32_16x16x32 consumes 16 rows x
+//    32 K of W (operand B: each lane loads 16 contiguous bytes of one row)
+//    and the matching 16 x 32 of x (operand A, batch rows >= B are zero), so
+//    W is streamed once for all B <= 16 rows of x, with 128-bit loads only.
+//  * K is split over up to 12 waves of the block (256 K per wave, every W
+//    load of a wave issued before the first MFMA), reduced through LDS. No
+//    cross-block reduction; at most 1024 blocks loop over the row tiles.
+//  * Fusions for the decoder step:
+//      norm_w != NULL   the input is RMSNorm(x) * norm_w (fastqwen3.py:108,114:
+//                       the block recomputes the 16 row statistics itself)
+//      residual != NULL residual <- T(residual + T(x W^T)) in place (the
+//                       `x = x + x_res` of fastqwen3.py:111,116)
+//      SwiGLU           W = [gate|up] interleaved in blocks of 32 rows; output
+//                       T(T(silu(T(g))) * T(u)) (eager silu(gate(x)) * up(x))
+//      bias + act       pre-activation rounded to T, activation in fp32
+//                       (fused_gemm.cuh:93-105)
+//      argmax           per-block (max, first index) over the 16 columns for
+//                       every batch row; tpp_argmax_partials finishes it.
 #include "tpp_common.hpp"
 
 namespace tpp {
 
-enum GemvEpi { kEpiPlain = 0, kEpiBiasAct = 1, kEpiSwiGLU = 2 };
+enum GemvEpi { kEpiPlain = 0, kEpiBiasAct = 1, kEpiSwiGLU = 2, kEpiResidual = 3 };
 
-constexpr int kGemvU = 2;                  // 64-K steps per load batch
-constexpr int kGemvKStep = 64 * kGemvU;    // K elements per load batch
+constexpr int kGemvWaveK = 256;   // K elements per wave and load batch
+constexpr int kGemvMaxWaves = 12; // 768 threads: 170 VGPRs per lane, no spills
 
 template <typename T>
 __device__ __forceinline__ typename VecT<T>::v8 ld16(const T *p, bool ok) {
@@ -46,7 +46,7 @@ __device__ __forceinline__ typename VecT<T>::v8 ld16(const T *p, bool ok) {
 template <typename T>
 __device__ __forceinline__ f32x4 mfma16(typename VecT<T>::v8 a, typename VecT<T>::v8 b,
                                         f32x4 c) {
-  if constexpr (sizeof(T) == 2 && __is_same(T, bf16))
+  if constexpr (__is_same(T, bf16))
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   else
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -60,277 +60,410 @@ __device__ __forceinline__ T epi_bias_act(float acc, const T *bias, int64_t n) {
   return from_f32<T>(apply_act<ACT>(pre));
 }
 
-template <typename T>
-__device__ __forceinline__ T epi_swiglu(float g, float u) {
+template <typename T> __device__ __forceinline__ T epi_swiglu(float g, float u) {
   const float gt = to_f32(from_f32<T>(g));
   const float s = to_f32(from_f32<T>(act_silu(gt)));
   const float ut = to_f32(from_f32<T>(u));
   return from_f32<T>(s * ut);
 }
 
-// grid.x: row tiles (16 weight rows; SwiGLU: 16 outputs = 16 gate + 16 up rows)
-// grid.y: K splits over blocks. block: 256 threads = 4 waves, each a K slice.
-template <typename T, int EPI, int ACT>
-__global__ __launch_bounds__(256) void gemv16_kernel(
-    const T *__restrict__ x, int64_t ldx, int NB, const T *__restrict__ W, int64_t N,
-    int64_t K, T *__restrict__ y, int64_t ldy, const T *__restrict__ bias,
-    float *__restrict__ ws, unsigned *__restrict__ cnt, int kslice, int nsplit) {
+// (value, index) "better than" with first-index ties and NaN as the maximum
+__device__ __forceinline__ bool am_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+struct GemvArgs {
+  const void *x;
+  int64_t ldx;
+  int NB;
+  const void *norm_w;
+  float eps;
+  const void *W;
+  int64_t N, K;
+  void *y;
+  int64_t ldy;
+  const void *bias;
+  void *residual; // [NB, N] in/out, ld = ldy
+  float *am_val;  // [tiles, NB] argmax partials (or null)
+  int *am_idx;
+  int kslice;
+};
+
+// Row tiles: 16 weight rows each (SwiGLU: 16 outputs from 16 gate + 16 up
+// rows). grid.x <= kGemvMaxBlocks blocks loop over the tiles, so the fused
+// input RMSNorm is computed once per block; block = 64 * nwaves threads,
+// wave w covers K slice w of every tile.
+constexpr int kGemvMaxBlocks = 1024;
+
+template <typename T, int EPI, int ACT, bool NORM, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t tiles) {
   typedef typename VecT<T>::v8 V8;
-  __shared__ f32x4 red[2][4][64];
-  const int lane = lane_id(), w = wave_id();
+  constexpr int NS = kGemvWaveK / 32; // MFMA steps per wave batch
+  __shared__ f32x4 red[EPI == kEpiSwiGLU ? 2 : 1][MAXW][64];
+  __shared__ float s_inv[16];
+  const int lane = lane_id(), w = wave_id(), nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t tile = blockIdx.x;
-  int64_t row0, row1 = 0;
-  if constexpr (EPI == kEpiSwiGLU) {
-    row0 = (tile >> 1) * 64 + (tile & 1) * 16;
-    row1 = row0 + 32;
-  } else {
-    row0 = tile * 16;
-  }
-  const int64_t k_begin = ((int64_t)blockIdx.y * 4 + w) * kslice;
-  const int64_t k_end = k_begin + kslice < K ? k_begin + kslice : K;
+  const int64_t N = a.N, K = a.K;
+  const T *X = (const T *)a.x;
+  const T *W = (const T *)a.W;
+  const bool xok = r < a.NB;
+  const T *xr = X + (xok ? r : 0) * a.ldx;
+  const int64_t k_begin = (int64_t)w * a.kslice;
+  const int64_t k_end = k_begin + a.kslice < K ? k_begin + a.kslice : K;
 
-  const bool xok = r < NB;
-  const T *xr = x + (xok ? r : 0) * ldx;
-  const bool w0ok = row0 + r < N;
-  const T *w0 = W + (w0ok ? row0 + r : 0) * K;
-  const bool w1ok = (EPI == kEpiSwiGLU) && (row1 + r < N);
-  const T *w1 = W + (w1ok ? row1 + r : 0) * K;
-
-  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  for (int64_t k = k_begin; k < k_end; k += kGemvKStep) {
-    V8 a[2 * kGemvU], b0[2 * kGemvU], b1[2 * kGemvU];
+  if constexpr (NORM) {
+    // inv_rms of the <= 16 input rows (wave w: rows w, w + nw, ..)
+    for (int row = w; row < a.NB; row += nw) {
+      const T *xp = X + row * a.ldx;
+      float ss = 0.f;
+      for (int64_t c = (int64_t)lane * 8; c < K; c += 64 * 8) {
+        float v[8];
+        load8(xp + c, v);
 #pragma unroll
-    for (int u = 0; u < 2 * kGemvU; ++u) {
+        for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) s_inv[row] = rsqrtf(ss / (float)K + a.eps);
+    }
+    __syncthreads();
+  }
+  // this wave's slice of the (normalised) input, reused by every tile
+  // kept resident when the wave's K slice is one load batch (K <= 4096 for
+  // plain GEMVs, 2048 for SwiGLU); longer slices reload x per batch
+  const bool x_res = k_end - k_begin <= kGemvWaveK;
+  V8 xa[NS];
+  auto load_x = [&](int64_t k, V8 (&dst)[NS]) {
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
       const int64_t c = k + u * 32 + g * 8; // K % 8 == 0: a chunk is all in or all out
-      const bool in = c < k_end;
-      b0[u] = ld16(w0 + c, in && w0ok);
-      if constexpr (EPI == kEpiSwiGLU) b1[u] = ld16(w1 + c, in && w1ok);
-      a[u] = ld16(xr + c, in && xok);
-    }
+      const bool ok = c < k_end && xok;
+      dst[u] = ld16(xr + c, ok);
+      if constexpr (NORM) {
+        if (ok) {
+          float xv[8], nv[8];
 #pragma unroll
-    for (int u = 0; u < 2 * kGemvU; ++u) {
-      acc0 = mfma16<T>(a[u], b0[u], acc0);
-      if constexpr (EPI == kEpiSwiGLU) acc1 = mfma16<T>(a[u], b1[u], acc1);
-    }
-  }
-  red[0][w][lane] = acc0;
-  if constexpr (EPI == kEpiSwiGLU) red[1][w][lane] = acc1;
-  __syncthreads();
-  if (w != 0) return;
-  acc0 = red[0][0][lane] + red[0][1][lane] + red[0][2][lane] + red[0][3][lane];
-  if constexpr (EPI == kEpiSwiGLU)
-    acc1 = red[1][0][lane] + red[1][1][lane] + red[1][2][lane] + red[1][3][lane];
-
-  // D layout of 16x16x32: lane -> column r (weight row), rows b = 4g + i.
-  const int64_t n0 = row0 + r, n1 = row1 + r;
-  if (nsplit > 1) {
+          for (int i = 0; i < 8; ++i) xv[i] = to_f32(dst[u][i]);
+          load8((const T *)a.norm_w + c, nv);
+          const float inv = s_inv[r];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int b = 4 * g + i;
-      if (b < NB) {
-        if (n0 < N) unsafeAtomicAdd(ws + (int64_t)b * N + n0, acc0[i]);
-        if constexpr (EPI == kEpiSwiGLU)
-          if (n1 < N) unsafeAtomicAdd(ws + (int64_t)b * N + n1, acc1[i]);
+          for (int i = 0; i < 8; ++i) dst[u][i] = from_f32<T>((xv[i] * inv) * nv[i]);
+        }
       }
     }
-    __threadfence();
-    unsigned prev = 0;
-    if (lane == 0) prev = atomicAdd(cnt + tile, 1u);
-    prev = __shfl(prev, 0, kWave);
-    if (prev != (unsigned)(nsplit - 1)) return;
-    __threadfence();
+  };
+  if (x_res) load_x(k_begin, xa);
+
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    int64_t row0, row1 = 0;
+    if constexpr (EPI == kEpiSwiGLU) {
+      row0 = (tile >> 1) * 64 + (tile & 1) * 16;
+      row1 = row0 + 32;
+    } else {
+      row0 = tile * 16;
+    }
+    const bool w0ok = row0 + r < N;
+    const T *w0 = W + (w0ok ? row0 + r : 0) * K;
+    const bool w1ok = (EPI == kEpiSwiGLU) && (row1 + r < N);
+    const T *w1 = W + (w1ok ? row1 + r : 0) * K;
+    // residual values this tile will update: fetched with the weights
+    float res_in[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (EPI == kEpiResidual) {
+      if (w == 0 && row0 + r < N) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int b = 4 * g + i;
-      if (b < NB) {
-        if (n0 < N) {
-          float *p = ws + (int64_t)b * N + n0;
-          acc0[i] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(p, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int i = 0; i < 4; ++i) {
+          const int b = 4 * g + i;
+          if (b < a.NB) res_in[i] = to_f32(((const T *)a.residual)[(int64_t)b * a.ldy + row0 + r]);
         }
+      }
+    }
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t k = k_begin; k < k_end; k += kGemvWaveK) {
+      V8 b0[NS], b1[NS];
+#pragma unroll
+      for (int u = 0; u < NS; ++u) {
+        const int64_t c = k + u * 32 + g * 8;
+        const bool in = c < k_end;
+        b0[u] = ld16(w0 + c, in && w0ok);
+        if constexpr (EPI == kEpiSwiGLU) b1[u] = ld16(w1 + c, in && w1ok);
+      }
+      V8 xl[NS];
+      if (!x_res) load_x(k, xl);
+#pragma unroll
+      for (int u = 0; u < NS; ++u) {
+        const V8 xv = x_res ? xa[u] : xl[u];
+        acc0 = mfma16<T>(xv, b0[u], acc0);
+        if constexpr (EPI == kEpiSwiGLU) acc1 = mfma16<T>(xv, b1[u], acc1);
+      }
+    }
+    red[0][w][lane] = acc0;
+    if constexpr (EPI == kEpiSwiGLU) red[1][w][lane] = acc1;
+    __syncthreads();
+    if (w == 0) {
+      acc0 = red[0][0][lane];
+      for (int i = 1; i < nw; ++i) acc0 += red[0][i][lane];
+      if constexpr (EPI == kEpiSwiGLU) {
+        acc1 = red[1][0][lane];
+        for (int i = 1; i < nw; ++i) acc1 += red[1][i][lane];
+      }
+      // D layout of 16x16x32: lane -> column r (weight row), rows b = 4g + i.
+      const int64_t n0 = row0 + r, n1 = row1 + r;
+      T *Y = (T *)a.y;
+      if (a.am_val) { // argmax partials over this tile's 16 columns
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float bv = n0 < N ? to_f32(from_f32<T>(acc0[i])) : -INFINITY;
+          int bix = n0 < N ? (int)n0 : 0x7fffffff;
+#pragma unroll
+          for (int sh = 1; sh < 16; sh <<= 1) {
+            const float ov = __shfl_xor(bv, sh, kWave);
+            const int oi = __shfl_xor(bix, sh, kWave);
+            if (am_better(ov, oi, bv, bix)) bv = ov, bix = oi;
+          }
+          const int b = 4 * g + i;
+          if (r == 0 && b < a.NB) {
+            a.am_val[tile * a.NB + b] = bv;
+            a.am_idx[tile * a.NB + b] = bix;
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = 4 * g + i;
+        if (b >= a.NB) continue;
         if constexpr (EPI == kEpiSwiGLU) {
-          if (n1 < N) {
-            float *p = ws + (int64_t)b * N + n1;
-            acc1[i] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(p, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (n0 < N && n1 < N) {
+            const int64_t on = (tile >> 1) * 32 + (tile & 1) * 16 + r;
+            Y[(int64_t)b * a.ldy + on] = epi_swiglu<T>(acc0[i], acc1[i]);
+          }
+        } else if (n0 < N) {
+          if constexpr (EPI == kEpiResidual) {
+            const float v = to_f32(from_f32<T>(acc0[i]));
+            ((T *)a.residual)[(int64_t)b * a.ldy + n0] = from_f32<T>(res_in[i] + v);
+          } else if constexpr (EPI == kEpiBiasAct) {
+            Y[(int64_t)b * a.ldy + n0] = epi_bias_act<T, ACT>(acc0[i], (const T *)a.bias, n0);
+          } else if (Y) {
+            Y[(int64_t)b * a.ldy + n0] = from_f32<T>(acc0[i]);
           }
         }
       }
     }
-    if (lane == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int b = 4 * g + i;
-    if (b >= NB) continue;
-    if constexpr (EPI == kEpiSwiGLU) {
-      if (n0 < N && n1 < N) {
-        const int64_t on = (tile >> 1) * 32 + (tile & 1) * 16 + r;
-        y[(int64_t)b * ldy + on] = epi_swiglu<T>(acc0[i], acc1[i]);
-      }
-    } else if (n0 < N) {
-      if constexpr (EPI == kEpiBiasAct)
-        y[(int64_t)b * ldy + n0] = epi_bias_act<T, ACT>(acc0[i], bias, n0);
-      else
-        y[(int64_t)b * ldy + n0] = from_f32<T>(acc0[i]);
-    }
+    __syncthreads(); // red[] is reused by the next tile
   }
 }
 
 // Generic fallback (any K, alignment, batch): one thread per output.
-template <typename T, int EPI, int ACT>
-__global__ __launch_bounds__(256) void gemv_scalar_kernel(
-    const T *__restrict__ x, int64_t ldx, int NB, const T *__restrict__ W, int64_t N,
-    int64_t K, T *__restrict__ y, int64_t ldy, const T *__restrict__ bias, int64_t NO) {
+template <typename T, int EPI, int ACT, bool NORM>
+__global__ __launch_bounds__(256) void gemv_scalar_kernel(GemvArgs a, int64_t NO) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= NO * NB) return;
+  if (t >= NO * a.NB) return;
   const int b = (int)(t / NO);
   const int64_t o = t - (int64_t)b * NO;
-  const T *xr = x + b * ldx;
+  const T *xr = (const T *)a.x + b * a.ldx;
+  const T *W = (const T *)a.W;
+  const int64_t K = a.K;
+  float inv = 1.f;
+  if constexpr (NORM) {
+    float ss = 0.f;
+    for (int64_t k = 0; k < K; ++k) ss += to_f32(xr[k]) * to_f32(xr[k]);
+    inv = rsqrtf(ss / (float)K + a.eps);
+  }
+  auto xin = [&](int64_t k) {
+    if constexpr (NORM) return to_f32(from_f32<T>((to_f32(xr[k]) * inv) * to_f32(((const T *)a.norm_w)[k])));
+    else return to_f32(xr[k]);
+  };
+  T *Y = (T *)a.y;
   if constexpr (EPI == kEpiSwiGLU) {
     const int64_t n0 = (o / 32) * 64 + (o % 32), n1 = n0 + 32;
-    float g = 0.f, u = 0.f;
+    float gs = 0.f, us = 0.f;
     for (int64_t k = 0; k < K; ++k) {
-      const float xv = to_f32(xr[k]);
-      g += xv * to_f32(W[n0 * K + k]);
-      u += xv * to_f32(W[n1 * K + k]);
+      const float xv = xin(k);
+      gs += xv * to_f32(W[n0 * K + k]);
+      us += xv * to_f32(W[n1 * K + k]);
     }
-    y[b * ldy + o] = epi_swiglu<T>(g, u);
+    Y[b * a.ldy + o] = epi_swiglu<T>(gs, us);
   } else {
     float acc = 0.f;
-    for (int64_t k = 0; k < K; ++k) acc += to_f32(xr[k]) * to_f32(W[o * K + k]);
-    if constexpr (EPI == kEpiBiasAct)
-      y[b * ldy + o] = epi_bias_act<T, ACT>(acc, bias, o);
-    else
-      y[b * ldy + o] = from_f32<T>(acc);
+    for (int64_t k = 0; k < K; ++k) acc += xin(k) * to_f32(W[o * K + k]);
+    if constexpr (EPI == kEpiResidual) {
+      T *res = (T *)a.residual + b * a.ldy + o;
+      *res = from_f32<T>(to_f32(*res) + to_f32(from_f32<T>(acc)));
+    } else if constexpr (EPI == kEpiBiasAct) {
+      Y[b * a.ldy + o] = epi_bias_act<T, ACT>(acc, (const T *)a.bias, o);
+    } else {
+      Y[b * a.ldy + o] = from_f32<T>(acc);
+    }
   }
 }
 
-struct GemvPlan {
-  bool vec;
-  int64_t tiles;
-  int kslice;
-  int nsplit;
-  size_t ws_bytes;
-};
-
-static GemvPlan plan_gemv(int64_t B, int64_t N, int64_t K, int epi, const void *x,
-                          const void *W, const void *y, int64_t ldx) {
-  GemvPlan p{};
-  p.vec = (K % 8 == 0) && (ldx % 8 == 0) && aligned16(x) && aligned16(W) && B <= 16;
-  if (!p.vec) return p;
-  p.tiles = (epi == kEpiSwiGLU) ? (N / 64) * 2 : (N + 15) / 16;
-  const int64_t steps = (K + kGemvKStep - 1) / kGemvKStep;
-  // aim for ~2048 waves in flight (8 per CU) without slicing below one step
-  int64_t want_waves = 2048 / (p.tiles > 0 ? p.tiles : 1);
-  if (want_waves < 4) want_waves = 4;
-  int64_t nsplit = (want_waves + 3) / 4;
-  if (nsplit > (steps + 3) / 4) nsplit = (steps + 3) / 4;
-  if (nsplit < 1) nsplit = 1;
-  const int64_t waves = nsplit * 4;
-  const int64_t steps_per_wave = (steps + waves - 1) / waves;
-  p.kslice = (int)(steps_per_wave * kGemvKStep);
-  p.nsplit = (int)((K + 4LL * p.kslice - 1) / (4LL * p.kslice));
-  p.ws_bytes = p.nsplit > 1 ? (size_t)(B * N) * 4 + (size_t)p.tiles * 4 : 0;
-  return p;
+// Final reduction of the argmax partials: out[b] = best over tiles.
+__global__ __launch_bounds__(1024) void argmax_partials_kernel(const float *__restrict__ val,
+                                                               const int *__restrict__ idx,
+                                                               int tiles, int NB,
+                                                               int64_t *__restrict__ out) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int b = blockIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int t = threadIdx.x; t < tiles; t += blockDim.x) {
+    const float v = val[(int64_t)t * NB + b];
+    const int i = idx[(int64_t)t * NB + b];
+    if (am_better(v, i, bv, bi)) bv = v, bi = i;
+  }
+#pragma unroll
+  for (int sh = 1; sh < kWave; sh <<= 1) {
+    const float ov = __shfl_xor(bv, sh, kWave);
+    const int oi = __shfl_xor(bi, sh, kWave);
+    if (am_better(ov, oi, bv, bi)) bv = ov, bi = oi;
+  }
+  if (lane_id() == 0) {
+    sv[wave_id()] = bv;
+    si[wave_id()] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x / kWave); ++w)
+      if (am_better(sv[w], si[w], bv, bi)) bv = sv[w], bi = si[w];
+    out[b] = bi;
+  }
 }
 
-template <typename T, int EPI, int ACT>
-static int launch_gemv(const void *x, int64_t ldx, int64_t B, const void *W, int64_t N,
-                       int64_t K, void *y, int64_t ldy, const void *bias, void *ws,
-                       size_t ws_bytes, hipStream_t st, const char *name) {
-  const GemvPlan p = plan_gemv(B, N, K, EPI, x, W, y, ldx);
-  const int64_t NO = (EPI == kEpiSwiGLU) ? N / 2 : N;
-  if (!p.vec) {
-    const int64_t blocks = (NO * B + 255) / 256;
-    gemv_scalar_kernel<T, EPI, ACT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
-        (const T *)x, ldx, (int)B, (const T *)W, N, K, (T *)y, ldy, (const T *)bias, NO);
+static bool gemv_vec_ok(const GemvArgs &a) {
+  return (a.K % 8 == 0) && (a.ldx % 8 == 0) && aligned16(a.x) && aligned16(a.W) &&
+         (a.norm_w == nullptr || aligned16(a.norm_w)) && a.NB <= 16;
+}
+
+template <typename T, int EPI, int ACT, bool NORM>
+static int launch_gemv(GemvArgs a, hipStream_t st, const char *name) {
+  const int64_t NO = (EPI == kEpiSwiGLU) ? a.N / 2 : a.N;
+  if (!gemv_vec_ok(a)) {
+    if (a.am_val) return set_error(TPP_E_UNSUPPORTED, "%s: argmax needs the vector path", name);
+    const int64_t blocks = (NO * a.NB + 255) / 256;
+    gemv_scalar_kernel<T, EPI, ACT, NORM><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a, NO);
     return check_launch(name);
   }
-  float *wsf = nullptr;
-  unsigned *cnt = nullptr;
-  if (p.nsplit > 1) {
-    if (!ws || ws_bytes < p.ws_bytes)
-      return set_error(TPP_E_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", name,
-                       p.ws_bytes, ws ? ws_bytes : (size_t)0);
-    if (!aligned16(ws)) return set_error(TPP_E_INVALID, "%s: workspace alignment", name);
-    wsf = (float *)ws;
-    cnt = (unsigned *)((char *)ws + (size_t)(B * N) * 4);
-  }
-  if (p.tiles > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: N too large", name);
-  gemv16_kernel<T, EPI, ACT><<<dim3((unsigned)p.tiles, (unsigned)p.nsplit), dim3(256), 0, st>>>(
-      (const T *)x, ldx, (int)B, (const T *)W, N, K, (T *)y, ldy, (const T *)bias, wsf, cnt,
-      p.kslice, p.nsplit);
+  const int64_t tiles = (EPI == kEpiSwiGLU) ? (a.N / 64) * 2 : (a.N + 15) / 16;
+  if (tiles > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: N too large", name);
+  // SwiGLU holds two W tiles per lane: cap its block at 8 waves (256 VGPRs)
+  constexpr int MAXW = EPI == kEpiSwiGLU ? 8 : kGemvMaxWaves;
+  int64_t nw = (a.K + kGemvWaveK - 1) / kGemvWaveK;
+  if (nw > MAXW) nw = MAXW;
+  if (nw < 1) nw = 1;
+  const int64_t per = (a.K + nw - 1) / nw;
+  a.kslice = (int)(((per + 31) / 32) * 32);
+  const int64_t blocks = tiles < kGemvMaxBlocks ? tiles : kGemvMaxBlocks;
+  gemv16_kernel<T, EPI, ACT, NORM, MAXW>
+      <<<dim3((unsigned)blocks), dim3((unsigned)(nw * 64)), 0, st>>>(a, tiles);
   return check_launch(name);
 }
 
-static int gemv_args(const char *name, const void *x, const void *W, const void *y, int64_t B,
-                     int64_t N, int64_t K, int64_t ldx, int64_t ldy) {
-  if (!x || !W || !y) return set_error(TPP_E_INVALID, "%s: null pointer", name);
+template <typename T, int EPI, int ACT>
+static int launch_gemv_n(const GemvArgs &a, hipStream_t st, const char *name) {
+  if (a.norm_w) return launch_gemv<T, EPI, ACT, true>(a, st, name);
+  return launch_gemv<T, EPI, ACT, false>(a, st, name);
+}
+
+static int gemv_args(const char *name, const void *x, const void *W, int64_t B, int64_t N,
+                     int64_t K, int64_t ldx) {
+  if (!x || !W) return set_error(TPP_E_INVALID, "%s: null pointer", name);
   if (B < 1 || N < 1 || K < 1)
     return set_error(TPP_E_INVALID, "%s: invalid shapes (B=%lld N=%lld K=%lld)", name,
                      (long long)B, (long long)N, (long long)K);
-  if (B > 16) return set_error(TPP_E_UNSUPPORTED, "%s: batch %lld > 16, use tpp_linear", name,
-                               (long long)B);
+  if (B > 16) return set_error(TPP_E_UNSUPPORTED, "%s: batch %lld > 16, use tpp_linear_act",
+                               name, (long long)B);
   if (ldx < K) return set_error(TPP_E_INVALID, "%s: ldx < K", name);
-  if (ldy < 1) return set_error(TPP_E_INVALID, "%s: ldy", name);
   return TPP_OK;
+}
+
+static GemvArgs make_gemv(const void *x, int64_t ldx, int64_t B, const void *norm_w, float eps,
+                          const void *W, int64_t N, int64_t K, void *y, int64_t ldy) {
+  GemvArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.NB = (int)B;
+  a.norm_w = norm_w;
+  a.eps = eps;
+  a.W = W;
+  a.N = N;
+  a.K = K;
+  a.y = y;
+  a.ldy = ldy;
+  return a;
 }
 
 } // namespace tpp
 
 using namespace tpp;
 
-extern "C" size_t tpp_gemv_workspace_size(int64_t B, int64_t N, int64_t K, int swiglu) {
-  // Conservative: assume the vector path (the scalar path needs none).
-  GemvPlan p = plan_gemv(B, N, K, swiglu ? kEpiSwiGLU : kEpiPlain, (void *)0, (void *)0,
-                         (void *)0, K);
-  return p.ws_bytes;
-}
-
 extern "C" int tpp_gemv(const void *x, const void *W, const void *bias, void *y, int64_t B,
                         int64_t N, int64_t K, int64_t ldx, int64_t ldy, int act, int dtype,
-                        void *workspace, size_t ws_bytes, void *stream) {
+                        void *stream) {
   const char *name = "tpp_gemv";
-  if (int e = gemv_args(name, x, W, y, B, N, K, ldx, ldy)) return e;
+  if (int e = gemv_args(name, x, W, B, N, K, ldx)) return e;
+  if (!y) return set_error(TPP_E_INVALID, "%s: null output", name);
   if (ldy < N) return set_error(TPP_E_INVALID, "%s: ldy < N", name);
   if (act < TPP_ACT_NONE || act > TPP_ACT_RELU)
     return set_error(TPP_E_INVALID, "%s: unknown activation %d", name, act);
+  GemvArgs a = make_gemv(x, ldx, B, nullptr, 0.f, W, N, K, y, ldy);
+  a.bias = bias;
   hipStream_t st = as_stream(stream);
   return TPP_DISPATCH_HALF(dtype, [&] {
-    if (!bias && act == TPP_ACT_NONE)
-      return launch_gemv<T, kEpiPlain, TPP_ACT_NONE>(x, ldx, B, W, N, K, y, ldy, nullptr,
-                                                     workspace, ws_bytes, st, name);
+    if (!bias && act == TPP_ACT_NONE) return launch_gemv_n<T, kEpiPlain, TPP_ACT_NONE>(a, st, name);
     switch (act) {
-    case TPP_ACT_GELU_TANH:
-      return launch_gemv<T, kEpiBiasAct, TPP_ACT_GELU_TANH>(x, ldx, B, W, N, K, y, ldy, bias,
-                                                            workspace, ws_bytes, st, name);
-    case TPP_ACT_SILU:
-      return launch_gemv<T, kEpiBiasAct, TPP_ACT_SILU>(x, ldx, B, W, N, K, y, ldy, bias,
-                                                       workspace, ws_bytes, st, name);
-    case TPP_ACT_RELU:
-      return launch_gemv<T, kEpiBiasAct, TPP_ACT_RELU>(x, ldx, B, W, N, K, y, ldy, bias,
-                                                       workspace, ws_bytes, st, name);
-    default:
-      return launch_gemv<T, kEpiBiasAct, TPP_ACT_NONE>(x, ldx, B, W, N, K, y, ldy, bias,
-                                                       workspace, ws_bytes, st, name);
+    case TPP_ACT_GELU_TANH: return launch_gemv_n<T, kEpiBiasAct, TPP_ACT_GELU_TANH>(a, st, name);
+    case TPP_ACT_SILU: return launch_gemv_n<T, kEpiBiasAct, TPP_ACT_SILU>(a, st, name);
+    case TPP_ACT_RELU: return launch_gemv_n<T, kEpiBiasAct, TPP_ACT_RELU>(a, st, name);
+    default: return launch_gemv_n<T, kEpiBiasAct, TPP_ACT_NONE>(a, st, name);
     }
   });
 }
 
-extern "C" int tpp_gemv_swiglu(const void *x, const void *W_gu, void *y, int64_t B,
-                               int64_t I, int64_t K, int64_t ldx, int64_t ldy, int dtype,
-                               void *workspace, size_t ws_bytes, void *stream) {
-  const char *name = "tpp_gemv_swiglu";
-  if (int e = gemv_args(name, x, W_gu, y, B, 2 * I, K, ldx, ldy)) return e;
-  if (I % 32 != 0)
-    return set_error(TPP_E_UNSUPPORTED, "%s: intermediate size %lld must be a multiple of 32",
-                     name, (long long)I);
-  if (ldy < I) return set_error(TPP_E_INVALID, "%s: ldy < I", name);
+extern "C" int tpp_gemv_fused(const void *x, const void *norm_w, float eps, const void *W,
+                              void *y, void *residual, int64_t B, int64_t N, int64_t K,
+                              int swiglu, int dtype, void *stream) {
+  const char *name = "tpp_gemv_fused";
+  if (int e = gemv_args(name, x, W, B, N, K, K)) return e;
+  if (swiglu && (N % 64 != 0))
+    return set_error(TPP_E_UNSUPPORTED, "%s: SwiGLU weight rows must be a multiple of 64", name);
+  if (swiglu && residual)
+    return set_error(TPP_E_INVALID, "%s: SwiGLU output cannot be added to a residual", name);
+  if (!residual && !y) return set_error(TPP_E_INVALID, "%s: no output", name);
+  const int64_t ldy = swiglu ? N / 2 : N;
+  GemvArgs a = make_gemv(x, K, B, norm_w, eps, W, N, K, y, ldy);
+  a.residual = residual;
   hipStream_t st = as_stream(stream);
   return TPP_DISPATCH_HALF(dtype, [&] {
-    return launch_gemv<T, kEpiSwiGLU, TPP_ACT_NONE>(x, ldx, B, W_gu, 2 * I, K, y, ldy, nullptr,
-                                                    workspace, ws_bytes, st, name);
+    if (swiglu) return launch_gemv_n<T, kEpiSwiGLU, TPP_ACT_NONE>(a, st, name);
+    if (residual) return launch_gemv_n<T, kEpiResidual, TPP_ACT_NONE>(a, st, name);
+    return launch_gemv_n<T, kEpiPlain, TPP_ACT_NONE>(a, st, name);
+  });
+}
+
+extern "C" size_t tpp_gemv_argmax_workspace_size(int64_t B, int64_t N) {
+  return (size_t)((N + 15) / 16) * (size_t)B * 8;
+}
+
+extern "C" int tpp_gemv_argmax(const void *x, const void *norm_w, float eps, const void *W,
+                               void *logits, int64_t *out_idx, int64_t B, int64_t N, int64_t K,
+                               int dtype, void *workspace, size_t ws_bytes, void *stream) {
+  const char *name = "tpp_gemv_argmax";
+  if (int e = gemv_args(name, x, W, B, N, K, K)) return e;
+  if (!out_idx) return set_error(TPP_E_INVALID, "%s: null index output", name);
+  if (N > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: N too large", name);
+  const int64_t tiles = (N + 15) / 16;
+  const size_t need = tpp_gemv_argmax_workspace_size(B, N);
+  if (!workspace || ws_bytes < need || !aligned16(workspace))
+    return set_error(TPP_E_WORKSPACE, "%s: workspace of %zu bytes required", name, need);
+  GemvArgs a = make_gemv(x, K, B, norm_w, eps, W, N, K, logits, N);
+  a.am_val = (float *)workspace;
+  a.am_idx = (int *)((char *)workspace + (size_t)tiles * B * 4);
+  hipStream_t st = as_stream(stream);
+  return TPP_DISPATCH_HALF(dtype, [&] {
+    if (int e = launch_gemv_n<T, kEpiPlain, TPP_ACT_NONE>(a, st, name)) return e;
+    argmax_partials_kernel<<<dim3((unsigned)B), dim3(1024), 0, st>>>(a.am_val, a.am_idx,
+                                                                     (int)tiles, (int)B, out_idx);
+    return check_launch(name);
   });
 }

@@ -8,10 +8,12 @@ it intends, down(silu(gate(x)) * up(x)) (the committed FFN feeds the
 3072-wide SiLU output into a 1024-input layer, fastqwen3.py:71-73).
 
 Execution:
-  * forward_impl keeps the residual stream in one buffer and fuses each
-    residual add into the next RMSNorm (one pass instead of three);
-    attention runs the fused QKV GEMM/GEMV -> QK-norm+RoPE+KV-append ->
-    flash/decode attention -> output projection chain.
+  * forward_impl keeps the residual stream in one buffer. For prefill it
+    fuses each residual add into the next RMSNorm; for <= 16 tokens
+    (decode) each RMSNorm is fused into the GEMV that reads it and each
+    residual add into the GEMV that writes it, so a layer is 6 kernels:
+    QKV GEMV, QK-norm+RoPE+KV-append, split-KV attention (+combine), o_proj
+    GEMV, SwiGLU GEMV, down GEMV.
   * GreedyDecoder captures one whole decode step (28 layers, lm_head,
     argmax, position advance) into a HIP graph and replays it per token, so
     the token loop issues one launch per token and never synchronises.
@@ -27,7 +29,8 @@ import torch.nn.functional as F
 
 from torchplusplus_amd._native import ext as _ext
 from torchplusplus_amd.attention.gqa import GroupedQueryAttention
-from torchplusplus_amd.dlops.linear import LinearSILU, interleave_gate_up, linear, swiglu
+from torchplusplus_amd.dlops.linear import (GEMV_MAX_ROWS, LinearSILU, interleave_gate_up,
+                                             linear, swiglu)
 from torchplusplus_amd.dlops.normalization import RmsNormFused
 from torchplusplus_amd.dlops.rope import compute_rope_params
 from torchplusplus_amd.llmops.kvcache import KVCache
@@ -149,6 +152,8 @@ class FastQwen3(LLMInference):
                      cache_position: Optional[int] = None, last_only: bool = False) -> torch.Tensor:
         blocks = self.transformer_blocs
         resid = F.embedding(input_ids, self.tok_embed.weight)  # residual stream, updated in place
+        if input_ids.numel() <= GEMV_MAX_ROWS:
+            return self._forward_small(resid, kv_caches, cache_position)
         h = blocks[0].rms_norm1(resid)
         for i, blk in enumerate(blocks):
             kv = kv_caches[i] if kv_caches is not None else None
@@ -161,6 +166,20 @@ class FastQwen3(LLMInference):
             h = h[:, -1:, :].contiguous()
         return linear(h, self.out_head.weight)
 
+    def _forward_small(self, resid, kv_caches, cache_position):
+        """<= 16 tokens (decode): every RMSNorm is fused into the GEMV that
+        consumes it and every residual add into the GEMV that produces it."""
+        for i, blk in enumerate(self.transformer_blocs):
+            at, n1, n2 = blk.attn, blk.rms_norm1, blk.rms_norm2
+            kv = kv_caches[i] if kv_caches is not None else None
+            qkv = _C.gemv_fused(resid, at.fused_qkv_weight(), n1.weight, n1.eps)
+            o = at.attend(qkv, self.cos, self.sin, kv, cache_position)
+            _C.gemv_fused(o, at.out_projection.weight, None, 1e-6, resid)
+            h = _C.gemv_swiglu(resid, blk.ffn.w_gu(), n2.weight, n2.eps)
+            _C.gemv_fused(h, blk.ffn.linear_layer2.weight, None, 1e-6, resid)
+        return _C.gemv_fused(resid, self.out_head.weight, self.final_rmsnorm.weight,
+                             self.final_rmsnorm.eps)
+
     @torch.inference_mode()
     def generate_greedy(self, input_ids: torch.Tensor, max_new_token: int,
                         use_graph: bool = True) -> torch.Tensor:
@@ -169,7 +188,7 @@ class FastQwen3(LLMInference):
         self.setup_kv_cache(seq_len + max_new_token, bsz)
         self.reset_kv_cache()
         logits = self.forward_impl(input_ids, self.kv_cache_array, 0, last_only=True)
-        first = _C.argmax_rows(logits[:, -1, :])
+        first = _C.argmax_rows(logits[:, -1, :].contiguous())
         dec = GreedyDecoder(self, bsz)
         toks = dec.run(first, seq_len, max_new_token - 1, use_graph=use_graph)
         return torch.cat([input_ids, first.view(bsz, 1), toks], dim=1)
@@ -195,21 +214,18 @@ class GreedyDecoder:
 
     def step(self):
         m, B = self.m, self.B
-        blocks = m.transformer_blocs
-        resid = F.embedding(self.ids, m.tok_embed.weight)  # [B, 1, E]
-        h = blocks[0].rms_norm1(resid)
-        for i, blk in enumerate(blocks):
-            at = blk.attn
+        resid = F.embedding(self.ids, m.tok_embed.weight)  # [B, 1, E], updated in place
+        for i, blk in enumerate(m.transformer_blocs):
+            at, n1, n2 = blk.attn, blk.rms_norm1, blk.rms_norm2
             kc, vc = self.caches[i].k_cache, self.caches[i].v_cache
-            q = at.project_rope_cache(h, m.cos, m.sin, kc, vc, self.positions)
+            qkv = _C.gemv_fused(resid, at.fused_qkv_weight(), n1.weight, n1.eps)
+            q = at.rope_cache(qkv, m.cos, m.sin, kc, vc, self.positions)
             o = _C.attn_decode(q, kc, vc, self.seqlens, 0.0, -1, None)
-            a = _C.gemv(o.view(B, 1, at.d_out), at.out_projection.weight, None, 0)
-            h = blk.rms_norm2.forward_add(a, resid)
-            f = _C.gemv(_C.gemv_swiglu(h, blk.ffn.w_gu()), blk.ffn.linear_layer2.weight, None, 0)
-            nxt = blocks[i + 1].rms_norm1 if i + 1 < len(blocks) else m.final_rmsnorm
-            h = nxt.forward_add(f, resid)
-        logits = _C.gemv(h, m.out_head.weight, None, 0)
-        tok = _C.argmax_rows(logits.view(B, -1))
+            _C.gemv_fused(o.view(B, 1, at.d_out), at.out_projection.weight, None, 1e-6, resid)
+            h = _C.gemv_swiglu(resid, blk.ffn.w_gu(), n2.weight, n2.eps)
+            _C.gemv_fused(h, blk.ffn.linear_layer2.weight, None, 1e-6, resid)
+        fn = m.final_rmsnorm
+        tok = _C.gemv_argmax(resid, m.out_head.weight, fn.weight, fn.eps, False)[0]
         self.ids.copy_(tok.view(B, 1))
         self.positions.add_(1)
         self.seqlens.add_(1)
