@@ -78,3 +78,16 @@ def test_compat_module_names_import():
 
     assert callable(rmsnormFused.rmsnormFused)
     assert callable(layernormFused.applyLayernorm)
+
+
+def test_torchpp_alias_imports_reference_paths():
+    """The reference's import paths (fastqwen3.py:7-11, tests/*.py) resolve."""
+    from torchpp.dlops.normalization import LayerNormFused, RmsNormFused  # noqa: F401
+    from torchpp.dlops.rope import compute_rope_params, qkrope_apply, rope_apply  # noqa: F401
+    from torchpp.dlops.fused_linear import LinearSILU  # noqa: F401
+    from torchpp.attention.gqa import GroupedQueryAttention  # noqa: F401
+    from torchpp.llmops.kvcache import KVCache
+    from torchpp.llmops.llm import LLMInference  # noqa: F401
+    import torchplusplus_amd.llmops.kvcache as real
+
+    assert KVCache is real.KVCache
