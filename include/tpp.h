@@ -180,6 +180,19 @@ int tpp_gemv_argmax(const void *x, const void *norm_w, float eps,
                     int64_t N, int64_t K, int dtype, void *workspace,
                     size_t ws_bytes, void *stream);
 
+/* One greedy decode step's tail: token[b] = argmax of RMSNorm(x)*norm_w . W^T
+ * (as tpp_gemv_argmax, no logits written), ids[b] = token[b], the next step's
+ * hidden row resid_next[b, :] = emb[token[b], :] (emb [vocab, K], vocab = N),
+ * positions[b] += 1 and seqlens[b] += 1 (either may be NULL). Replaces the
+ * sample_greedy -> torch.cat -> tok_emb -> pos += 1 tail of the generation
+ * loop (torchpp/llmops/llm.py:181-186, 226-236; fastqwen3.py:165-188).
+ * Workspace as tpp_gemv_argmax_workspace_size(B, N). */
+int tpp_greedy_step(const void *x, const void *norm_w, float eps,
+                    const void *W, const void *emb, int64_t *ids,
+                    void *resid_next, int32_t *positions, int32_t *seqlens,
+                    int64_t B, int64_t N, int64_t K, int dtype,
+                    void *workspace, size_t ws_bytes, void *stream);
+
 /* ---- attention ----------------------------------------------------------- */
 
 /* Flash attention forward, the flash_attn_func contract used by the reference
@@ -220,6 +233,25 @@ int tpp_attn_decode(const void *q, const void *k_cache, const void *v_cache,
                     int64_t D, int64_t Lmax, float softmax_scale,
                     int window_left, int dtype, void *workspace,
                     size_t ws_bytes, void *stream);
+
+/* Decode attention with the per-layer prologue fused in (replaces
+ * tpp_qkv_rope_cache + tpp_attn_decode for one new token per sequence): the
+ * new token's raw projection qkv [B, (Hq + 2*Hkv) * D] is split into heads,
+ * q and k get RMSNorm over D (q_norm_w / k_norm_w, NULL = none) and RoPE at
+ * position seqlens[b] - 1 (tables cos/sin [ctx, D] of type cs_dtype), the new
+ * k and v are written into the caches at that position, and the query
+ * attends to keys [0, seqlens[b]) (the cache prefix plus the new key).
+ * Caches/o/workspace as in tpp_attn_decode; seqlens is required. */
+int tpp_attn_decode_fused(const void *qkv, const void *q_norm_w,
+                          const void *k_norm_w, const void *cos,
+                          const void *sin, int64_t ctx, int cs_dtype, float eps,
+                          void *k_cache, void *v_cache, void *o,
+                          const int64_t *k_strides, const int64_t *v_strides,
+                          const int64_t *o_strides, const int32_t *seqlens,
+                          int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                          int64_t Lmax, float softmax_scale, int window_left,
+                          int dtype, void *workspace, size_t ws_bytes,
+                          void *stream);
 
 /* ---- sampling ------------------------------------------------------------ */
 

@@ -115,3 +115,31 @@ def test_decode_window_and_matches_prefill_path(dev):
                         vc[:1, :, :300].transpose(1, 2).to(dev), causal=True)
     d0 = decode_attention(q[:1].to(dev), kc[:1].to(dev), vc[:1].to(dev))
     close(p, d0, atol=1e-2, rtol=1e-2, what="decode vs prefill kernel")
+
+
+@pytest.mark.parametrize("hq,hkv,norm", [(16, 8, True), (8, 1, True), (4, 4, False)])
+def test_decode_fused_prologue_matches_unfused(dev, hq, hkv, norm):
+    """attn_decode_fused == qkv_rope_cache + attn_decode: same caches (bit-exact)
+    and the same attention output, for ragged positions."""
+    from torchplusplus_amd._native import ext
+
+    C = ext()
+    g = torch.Generator().manual_seed(9)
+    B, D, Lmax = 4, 128, 600
+    qkv = torch.randn(B, 1, (hq + 2 * hkv) * D, generator=g).bfloat16().to(dev)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16().to(dev) if norm else None
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16().to(dev) if norm else None
+    cos, sin = oracle.compute_rope_params(D, 1e6, 1024)
+    cos, sin = cos.to(dev), sin.to(dev)
+    kc = torch.randn(B, hkv, Lmax, D, generator=g).bfloat16().to(dev)
+    vc = torch.randn(B, hkv, Lmax, D, generator=g).bfloat16().to(dev)
+    pos = torch.tensor([0, 5, 299, 599], dtype=torch.int32).to(dev)
+    kc2, vc2 = kc.clone(), vc.clone()
+    q = torch.empty(B, 1, hq, D, dtype=torch.bfloat16, device=dev)
+    C.qkv_rope_cache(qkv, q, kc2, vc2, qw, kw, cos, sin, pos, 1e-6)
+    ref = C.attn_decode(q, kc2, vc2, pos + 1, 0.0, -1, None)
+    got = C.attn_decode_fused(qkv, qw, kw, cos, sin, 1e-6, kc, vc, pos + 1)
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2), "cache append differs"
+    close(got, ref, atol=1e-2, rtol=1e-2, what="fused decode")
+    e = oracle.decode_attention(q.cpu(), kc2.cpu(), vc2.cpu(), (pos + 1).tolist())
+    close(got, e, what="fused decode vs oracle")

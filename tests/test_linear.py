@@ -156,6 +156,33 @@ def test_gemv_argmax_lm_head(dev, bsz, n):
     assert len(only) == 1 and torch.equal(only[0], idx)
 
 
+@pytest.mark.parametrize("n", [5000, 40000])
+def test_greedy_step_tail(dev, n):
+    """argmax -> ids, next embedding gathered into the residual row, and the
+    position/length advance, in one call (llm.py:181-186, 226-236)."""
+    bsz, k = 8, 1024
+    x, w, _ = _mk(bsz, n, k, torch.bfloat16, seed=16)
+    nw = (1 + 0.1 * torch.randn(k, generator=torch.Generator().manual_seed(17))).bfloat16()
+    emb = torch.randn(n, k, generator=torch.Generator().manual_seed(18)).bfloat16()
+    # a duplicated, dominant row pair: the first index must win across blocks
+    w[3] *= 8
+    w[n - 7] = w[3]
+    xd, wd, nwd = x.to(dev), w.to(dev), nw.to(dev)
+    want, logits = ext().gemv_argmax(xd, wd, nwd, 1e-6, True)
+    e = oracle.linear_act(oracle.rmsnorm(x, nw, 1e-6), w)
+    close(logits, e, what="lm_head logits")
+    assert torch.equal(want.cpu(), torch.argmax(logits.cpu().float(), dim=-1))
+    ids = torch.full((bsz, 1), -1, dtype=torch.long, device=dev)
+    resid = xd.clone()
+    pos = torch.arange(bsz, dtype=torch.int32, device=dev)
+    sl = pos + 1
+    ext().greedy_step(resid, wd, nwd, 1e-6, emb.to(dev), ids, resid, pos, sl)
+    assert torch.equal(ids.view(-1), want)
+    assert torch.equal(resid.cpu(), emb[want.cpu()])
+    assert pos.cpu().tolist() == list(range(1, bsz + 1))
+    assert sl.cpu().tolist() == list(range(2, bsz + 2))
+
+
 def test_argmax_first_index_on_ties(dev):
     x = torch.zeros(2, 1000).bfloat16()
     x[0, [5, 700]] = 3.0

@@ -73,6 +73,15 @@ class GroupedQueryAttention(nn.Module):
                           cos, sin, positions, eps)
         return q
 
+    def decode_fused(self, qkv, cos, sin, k_cache, v_cache, seqlens):
+        """One new token per sequence: QK-norm + RoPE at position seqlens-1,
+        K/V appended to the caches, split-KV attention over seqlens keys;
+        returns [B, 1, Hq, D]."""
+        eps = self.q_norm.eps if self.q_norm is not None and self.q_norm.eps is not None else 1e-6
+        return _C.attn_decode_fused(qkv, self.q_norm.weight if self.q_norm is not None else None,
+                                    self.k_norm.weight if self.k_norm is not None else None,
+                                    cos, sin, eps, k_cache, v_cache, seqlens)
+
     def attend(self, qkv, cos, sin, kv_cache: Optional[KVCache] = None,
                cache_pos: Optional[int] = None) -> torch.Tensor:
         """Steps 2-3: rope/cache the projected qkv and attend; returns the
@@ -82,10 +91,17 @@ class GroupedQueryAttention(nn.Module):
         if kv_cache is not None:
             start = kv_cache.cache_len if cache_pos is None else int(cache_pos)
             kv_cache.ensure(bs, start + seq_len)
+            total = start + seq_len
+            if seq_len == 1 and kv_cache.k_cache.shape[0] == bs:
+                # one new token: QK-norm + RoPE + cache append fused into the
+                # split-KV decode kernel
+                seqlens = torch.full((bs,), total, dtype=torch.int32, device=dev)
+                kv_cache.cache_len = max(kv_cache.cache_len, total)
+                return self.decode_fused(qkv, cos, sin, kv_cache.k_cache, kv_cache.v_cache,
+                                         seqlens).reshape(bs, seq_len, self.d_out)
             positions = torch.full((bs,), start, dtype=torch.int32, device=dev)
             q = self.rope_cache(qkv, cos, sin, kv_cache.k_cache, kv_cache.v_cache, positions)
             kv_cache.cache_len = max(kv_cache.cache_len, start + seq_len)
-            total = start + seq_len
             if seq_len == 1:
                 seqlens = torch.full((bs,), total, dtype=torch.int32, device=dev)
                 o = decode_attention(q, kv_cache.k_cache, kv_cache.v_cache, seqlens)

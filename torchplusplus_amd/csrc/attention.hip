@@ -49,6 +49,17 @@ struct AttnArgs {
   int left, right;  // window, -1 = unbounded; causal => right = 0
 };
 
+// Optional fused decode prologue: the new token's raw QKV projection, QK
+// RMSNorm weights and RoPE tables. When set, the decode kernel normalises and
+// rotates q itself and appends the new key/value to the cache.
+struct DecodeFuse {
+  const void *qkv; // [B, (Hq + 2 Hkv) * D]
+  const void *qw, *kw;
+  const void *cos, *sin;
+  int cs_dtype, ctx;
+  float eps;
+};
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kKvTile = 64;
 
@@ -336,38 +347,101 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(AttnArgs p, int D) {
 // softmax is updated once per batch of passes.
 // ---------------------------------------------------------------------------
 constexpr int kDecMaxG = 8;
-constexpr int kDecU = 8;
+constexpr int kDecU = 4; // key passes per load batch (two batches in flight)
 
 constexpr int kDecMaxSplit = 256;
 
-template <typename T, int D, int G>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int *__restrict__ seqlens,
-                                                          int fixed_len, float *__restrict__ ws_o,
-                                                          float *__restrict__ ws_ml, int chunk,
-                                                          int nsplit) {
+// RMSNorm (optional) + rotate-half RoPE of one head row held as 8 values per
+// lane by LPK lanes (lane dp owns d = 8 dp .. 8 dp + 7), rounded to T at the
+// same points as the unfused path (norm output, rotated output).
+template <typename T, int LPK>
+__device__ __forceinline__ void norm_rope_row(float (&x)[8], const T *nw, float eps,
+                                              const DecodeFuse &f, int pos, int dp) {
+  constexpr int D = LPK * 8;
+  if (nw) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+    ss = group_sum<LPK>(ss);
+    const float inv = rsqrtf(ss / (float)D + eps);
+    float w[8];
+    load8(nw + dp * 8, w);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = to_f32(from_f32<T>((x[j] * inv) * w[j]));
+  }
+  float pt[8], c[8], sn[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pt[j] = __shfl_xor(x[j], LPK / 2, kWave); // d +- D/2
+  const int pr = pos < 0 ? 0 : (pos < f.ctx ? pos : f.ctx - 1);
+  load_cs8_rt(f.cos, (int64_t)pr * D + dp * 8, f.cs_dtype, c);
+  load_cs8_rt(f.sin, (int64_t)pr * D + dp * 8, f.cs_dtype, sn);
+  const float sgn = dp < LPK / 2 ? -1.f : 1.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = to_f32(from_f32<T>(x[j] * c[j] + sgn * pt[j] * sn[j]));
+}
+
+template <typename T, int D, int G, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const int *__restrict__ seqlens,
+                                                              int fixed_len, float *__restrict__ ws_o,
+                                                              float *__restrict__ ws_ml, int chunk,
+                                                              int nsplit, DecodeFuse fz) {
   typedef typename VecT<T>::v8 V8;
   constexpr int LPK = D / 8;        // lanes per key
   constexpr int KPW = kWave / LPK;  // keys per wave pass
   constexpr int U = kDecU;
-  __shared__ float red_m[4][G], red_l[4][G];
-  __shared__ float red_o[4][G][D];
+  __shared__ float red_m[NW][G], red_l[NW][G];
+  __shared__ float red_o[NW][G][D];
 
   const int lane = lane_id(), w = wave_id();
   const int row = lane / LPK, dp = lane % LPK;
   const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
-  int L = seqlens ? seqlens[b] : fixed_len;
-  L = L < p.Sk ? (L > 0 ? L : 0) : p.Sk; // never read past the cache
+  const int Lraw = seqlens ? seqlens[b] : fixed_len;
+  const int L = Lraw < p.Sk ? (Lraw > 0 ? Lraw : 0) : p.Sk; // never read past the cache
   int lo = 0;
   if (p.left >= 0) lo = L - 1 - p.left > 0 ? L - 1 - p.left : 0;
   int k_begin = split * chunk, k_end = k_begin + chunk;
   k_begin = k_begin > lo ? k_begin : lo;
   k_end = k_end < L ? k_end : L;
+  // fused prologue: position L-1 is the new token; this block attends to it
+  // from registers (if it falls in its chunk) and the cache loop stops before it
+  const bool fused = fz.qkv != nullptr;
+  const int pnew = L - 1;
+  const bool own_new = fused && Lraw <= p.Sk && pnew >= k_begin && pnew < k_end;
+  if (fused && k_end > pnew) k_end = pnew;
+  const T *qkv_row = fused ? (const T *)fz.qkv + (int64_t)b * (p.Hq + 2 * p.Hkv) * D : nullptr;
+  const T *kp = (const T *)p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + dp * 8;
+  const T *vp = (const T *)p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh + dp * 8;
+  V8 zero;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) zero[i] = (T)0.0f;
+
+  // Software-pipelined key loop: the K/V loads of batch i+1 are in flight
+  // while batch i is scored, so a wave waits for memory once, not per batch.
+  constexpr int STRIDE = NW * KPW * U; // keys per block-wide batch
+  auto load_batch = [&](int base, V8 (&kr)[U], V8 (&vr)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key = base + u * NW * KPW + row;
+      const bool ok = key < k_end;
+      kr[u] = ok ? *reinterpret_cast<const V8 *>(kp + (int64_t)key * p.k_ss) : zero;
+      vr[u] = ok ? *reinterpret_cast<const V8 *>(vp + (int64_t)key * p.v_ss) : zero;
+    }
+  };
+  // the first K/V batch is requested before the q prologue's dependent loads
+  const int first = k_begin + w * KPW;
+  V8 ka[U], va[U], kb[U], vb[U];
+  if (first < k_end) load_batch(first, ka, va);
 
   float qv[G][8];
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) {
-    const T *qp = (const T *)p.q + (int64_t)b * p.q_sb + (int64_t)(hk * G + gi) * p.q_sh + dp * 8;
-    load8(qp, qv[gi]);
+    if (fused) {
+      load8(qkv_row + (int64_t)(hk * G + gi) * D + dp * 8, qv[gi]);
+      norm_rope_row<T, LPK>(qv[gi], (const T *)fz.qw, fz.eps, fz, pnew, dp);
+    } else {
+      const T *qp = (const T *)p.q + (int64_t)b * p.q_sb + (int64_t)(hk * G + gi) * p.q_sh + dp * 8;
+      load8(qp, qv[gi]);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) qv[gi][j] *= p.scale_log2;
   }
@@ -379,25 +453,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int 
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[gi][j] = 0.f;
   }
-  const T *kp = (const T *)p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + dp * 8;
-  const T *vp = (const T *)p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh + dp * 8;
-  V8 zero;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) zero[i] = (T)0.0f;
-
-  for (int base = k_begin + w * KPW; base < k_end; base += 4 * KPW * U) {
-    V8 kr[U], vr[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int key = base + u * 4 * KPW + row;
-      const bool ok = key < k_end;
-      kr[u] = ok ? *reinterpret_cast<const V8 *>(kp + (int64_t)key * p.k_ss) : zero;
-      vr[u] = ok ? *reinterpret_cast<const V8 *>(vp + (int64_t)key * p.v_ss) : zero;
-    }
+  auto compute_batch = [&](int base, const V8 (&kr)[U], const V8 (&vr)[U]) {
     float sc[U][G];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const bool ok = base + u * 4 * KPW + row < k_end;
+      const bool ok = base + u * NW * KPW + row < k_end;
       float kf[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) kf[j] = to_f32(kr[u][j]);
@@ -432,6 +492,43 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int 
       }
       m[gi] = mb;
     }
+  };
+  if (first < k_end) {
+    for (int base = first; base < k_end; base += 2 * STRIDE) {
+      const bool more = base + STRIDE < k_end;
+      if (more) load_batch(base + STRIDE, kb, vb);
+      compute_batch(base, ka, va);
+      if (!more) break;
+      if (base + 2 * STRIDE < k_end) load_batch(base + 2 * STRIDE, ka, va);
+      compute_batch(base + STRIDE, kb, vb);
+    }
+  }
+  if (own_new && w == 0) {
+    // the new key/value: normalise + rotate k, append both to the cache (row
+    // 0 lanes), and fold the key into row 0's online softmax
+    float kf[8], vf[8];
+    load8(qkv_row + (int64_t)(p.Hq + hk) * D + dp * 8, kf);
+    load8(qkv_row + (int64_t)(p.Hq + p.Hkv + hk) * D + dp * 8, vf);
+    norm_rope_row<T, LPK>(kf, (const T *)fz.kw, fz.eps, fz, pnew, dp);
+    if (row == 0) {
+      store8((T *)kp + (int64_t)pnew * p.k_ss, kf);
+      store8((T *)vp + (int64_t)pnew * p.v_ss, vf);
+    }
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      float sdot = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sdot += qv[gi][j] * kf[j];
+      sdot = group_sum<LPK>(sdot);
+      if (row == 0) {
+        const float mn = fmaxf(m[gi], sdot);
+        const float a = exp2f(m[gi] - mn), e = exp2f(sdot - mn);
+        l[gi] = l[gi] * a + e;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[gi][j] = acc[gi][j] * a + e * to_f32(from_f32<T>(vf[j]));
+        m[gi] = mn;
+      }
+    }
   }
   // merge the KPW key rows of the wave (lanes with equal dp)
 #pragma unroll
@@ -461,21 +558,27 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int 
     }
   }
   __syncthreads();
-  // merge the 4 waves: thread -> (gi, d); write this chunk's partial
+  // merge the NW waves: thread -> (gi, d); write this chunk's partial, or the
+  // final output when the whole key range is one chunk
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int gi = idx / D, d = idx % D;
     float mx = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) mx = fmaxf(mx, red_m[ww][gi]);
+    for (int ww = 0; ww < NW; ++ww) mx = fmaxf(mx, red_m[ww][gi]);
     const float mu = mx == -INFINITY ? 0.f : mx;
     float ls = 0.f, os = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
+    for (int ww = 0; ww < NW; ++ww) {
       const float c = exp2f(red_m[ww][gi] - mu);
       ls += red_l[ww][gi] * c;
       os += red_o[ww][gi][d] * c;
     }
     const int hq = hk * G + gi;
+    if (nsplit == 1) {
+      T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
+      op[d] = from_f32<T>(ls > 0.f ? os / ls : 0.f);
+      continue;
+    }
     const int64_t slot = ((int64_t)b * p.Hq + hq) * nsplit + split;
     ws_o[slot * D + d] = os;
     if (d == 0) {
@@ -491,45 +594,50 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs p, const int 
 // which on MI355X write back / invalidate the XCD's L2 (the 8 XCD L2s are not
 // coherent) and cost far more than a kernel boundary.
 template <typename T, int D, int G>
-__global__ __launch_bounds__(256) void attn_decode_merge_kernel(AttnArgs p,
-                                                                const float *__restrict__ ws_o,
-                                                                const float *__restrict__ ws_ml,
-                                                                int nsplit) {
+__global__ __launch_bounds__(G * D) void attn_decode_merge_kernel(AttnArgs p,
+                                                                  const float *__restrict__ ws_o,
+                                                                  const float *__restrict__ ws_ml,
+                                                                  int nsplit) {
+  constexpr int PRE = 16; // partial outputs prefetched per thread
   __shared__ float s_w[G][kDecMaxSplit], s_l[G][kDecMaxSplit], s_inv[G];
   const int hk = blockIdx.x, b = blockIdx.y, lane = lane_id(), w = wave_id();
+  const int gi = threadIdx.x / D, d = threadIdx.x % D;
   const int64_t s0 = ((int64_t)b * p.Hq + hk * G) * nsplit; // slot of (gi = 0, split 0)
+  // this thread's partial outputs do not depend on the weights: load first
+  const float *po = ws_o + (s0 + (int64_t)gi * nsplit) * D + d;
+  float pre[PRE];
+#pragma unroll
+  for (int j = 0; j < PRE; ++j) pre[j] = j < nsplit ? po[(int64_t)j * D] : 0.f;
   for (int idx = threadIdx.x; idx < G * nsplit; idx += blockDim.x) {
-    const int gi = idx / nsplit, sp = idx % nsplit;
-    const float *ml = ws_ml + (s0 + (int64_t)gi * nsplit + sp) * 2;
-    s_w[gi][sp] = ml[0];
-    s_l[gi][sp] = ml[1];
+    const int g2 = idx / nsplit, sp = idx % nsplit;
+    const float *ml = ws_ml + (s0 + (int64_t)g2 * nsplit + sp) * 2;
+    s_w[g2][sp] = ml[0];
+    s_l[g2][sp] = ml[1];
   }
   __syncthreads();
-  for (int gi = w; gi < G; gi += 4) { // one wave per query head
+  const int nwave = blockDim.x / kWave;
+  for (int g2 = w; g2 < G; g2 += nwave) { // one wave per query head
     float mx = -INFINITY;
-    for (int sp = lane; sp < nsplit; sp += kWave) mx = fmaxf(mx, s_w[gi][sp]);
+    for (int sp = lane; sp < nsplit; sp += kWave) mx = fmaxf(mx, s_w[g2][sp]);
 #pragma unroll
     for (int sh = 1; sh < kWave; sh <<= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, kWave));
     const float mu = mx == -INFINITY ? 0.f : mx;
     float ls = 0.f;
     for (int sp = lane; sp < nsplit; sp += kWave) {
-      const float wgt = exp2f(s_w[gi][sp] - mu);
-      s_w[gi][sp] = wgt;
-      ls += wgt * s_l[gi][sp];
+      const float wgt = exp2f(s_w[g2][sp] - mu);
+      s_w[g2][sp] = wgt;
+      ls += wgt * s_l[g2][sp];
     }
     ls = wave_sum(ls);
-    if (lane == 0) s_inv[gi] = ls > 0.f ? 1.f / ls : 0.f;
+    if (lane == 0) s_inv[g2] = ls > 0.f ? 1.f / ls : 0.f;
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const int gi = idx / D, d = idx % D;
-    const float *po = ws_o + (s0 + (int64_t)gi * nsplit) * D + d;
-    float os = 0.f;
-#pragma unroll 8
-    for (int sp = 0; sp < nsplit; ++sp) os += s_w[gi][sp] * po[(int64_t)sp * D];
-    T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)(hk * G + gi) * p.o_sh;
-    op[d] = from_f32<T>(os * s_inv[gi]);
-  }
+  float os = 0.f;
+#pragma unroll
+  for (int j = 0; j < PRE; ++j) os += j < nsplit ? s_w[gi][j] * pre[j] : 0.f;
+  for (int sp = PRE; sp < nsplit; ++sp) os += s_w[gi][sp] * po[(int64_t)sp * D];
+  T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)(hk * G + gi) * p.o_sh;
+  op[d] = from_f32<T>(os * s_inv[gi]);
 }
 
 static int check_attn(const char *name, const AttnArgs &a, int64_t D) {
@@ -573,51 +681,73 @@ static int launch_prefill(const AttnArgs &a, int64_t D, hipStream_t st, const ch
 }
 
 struct DecodePlan {
-  int chunk, nsplit;
+  int chunk, nsplit, nw;
   size_t ws_bytes;
 };
 
+// Split-KV plan: about one 8-wave block per CU, each (batch, KV head) pair's
+// keys split into whole load batches; one split needs no merge kernel.
 static DecodePlan plan_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t Lmax) {
   DecodePlan pl{};
-  const int64_t keys_per_batch = 4 * (kWave / (D / 8)) * kDecU; // one load batch per wave
-  int64_t chunk = keys_per_batch;
-  while ((Lmax + chunk - 1) / chunk > kDecMaxSplit) chunk += keys_per_batch;
+  const int64_t kpw = kWave / (D / 8);
+  const int64_t pairs = B * Hkv > 0 ? B * Hkv : 1;
+  pl.nw = (Hkv > 0 && Hq / Hkv <= 2) ? 8 : 4; // more query heads per KV head: more VGPRs
+  const int64_t batch = pl.nw * kpw * kDecU; // keys per block-wide load batch
+  // about 2048 waves (8 per CU), in whole load batches
+  int64_t want = (2048 / pl.nw + pairs - 1) / pairs;
+  int64_t chunk = (Lmax + want - 1) / want;
+  chunk = ((chunk + batch - 1) / batch) * batch;
+  if (chunk < batch) chunk = batch;
+  while ((Lmax + chunk - 1) / chunk > kDecMaxSplit) chunk += batch;
   pl.chunk = (int)chunk;
   pl.nsplit = (int)((Lmax + chunk - 1) / chunk);
   if (pl.nsplit < 1) pl.nsplit = 1;
-  pl.ws_bytes = (size_t)(B * Hq * pl.nsplit) * (size_t)(D + 2) * sizeof(float);
+  pl.ws_bytes = pl.nsplit > 1 ? (size_t)(B * Hq * pl.nsplit) * (size_t)(D + 2) * sizeof(float) : 16;
   return pl;
 }
 
 template <typename T, int D, int G>
 static void launch_decode_g(const AttnArgs &a, dim3 grid, const int *seqlens, int L, float *ws_o,
-                            float *ws_ml, const DecodePlan &pl, hipStream_t st) {
-  attn_decode_kernel<T, D, G><<<grid, dim3(256), 0, st>>>(a, seqlens, L, ws_o, ws_ml, pl.chunk,
-                                                         pl.nsplit);
-  attn_decode_merge_kernel<T, D, G><<<dim3(grid.y, grid.z), dim3(256), 0, st>>>(a, ws_o, ws_ml,
-                                                                               pl.nsplit);
+                            float *ws_ml, const DecodePlan &pl, const DecodeFuse &fz,
+                            hipStream_t st) {
+  if constexpr (G <= 2) {
+    if (pl.nw == 8) {
+      attn_decode_kernel<T, D, G, 8><<<grid, dim3(512), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
+                                                                 pl.chunk, pl.nsplit, fz);
+    } else {
+      attn_decode_kernel<T, D, G, 4><<<grid, dim3(256), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
+                                                                 pl.chunk, pl.nsplit, fz);
+    }
+  } else
+    attn_decode_kernel<T, D, G, 4><<<grid, dim3(256), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
+                                                               pl.chunk, pl.nsplit, fz);
+  if (pl.nsplit > 1)
+    attn_decode_merge_kernel<T, D, G><<<dim3(grid.y, grid.z), dim3(G * D), 0, st>>>(
+        a, ws_o, ws_ml, pl.nsplit);
 }
 
 template <typename T, int D>
 static void launch_decode_d(const AttnArgs &a, int G, dim3 grid, const int *seqlens, int L,
-                            float *ws_o, float *ws_ml, const DecodePlan &pl, hipStream_t st) {
+                            float *ws_o, float *ws_ml, const DecodePlan &pl, const DecodeFuse &fz,
+                            hipStream_t st) {
   switch (G) {
-  case 1: launch_decode_g<T, D, 1>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
-  case 2: launch_decode_g<T, D, 2>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
-  case 3: launch_decode_g<T, D, 3>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
-  case 4: launch_decode_g<T, D, 4>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
-  case 5: launch_decode_g<T, D, 5>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
-  case 6: launch_decode_g<T, D, 6>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
-  case 7: launch_decode_g<T, D, 7>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
-  default: launch_decode_g<T, D, 8>(a, grid, seqlens, L, ws_o, ws_ml, pl, st); break;
+  case 1: launch_decode_g<T, D, 1>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
+  case 2: launch_decode_g<T, D, 2>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
+  case 3: launch_decode_g<T, D, 3>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
+  case 4: launch_decode_g<T, D, 4>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
+  case 5: launch_decode_g<T, D, 5>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
+  case 6: launch_decode_g<T, D, 6>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
+  case 7: launch_decode_g<T, D, 7>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
+  default: launch_decode_g<T, D, 8>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
   }
 }
 
 template <typename T>
 static void launch_decode(const AttnArgs &a, int64_t D, int G, dim3 grid, const int *seqlens,
-                          int L, float *ws_o, float *ws_ml, const DecodePlan &pl, hipStream_t st) {
-  if (D == 128) launch_decode_d<T, 128>(a, G, grid, seqlens, L, ws_o, ws_ml, pl, st);
-  else launch_decode_d<T, 64>(a, G, grid, seqlens, L, ws_o, ws_ml, pl, st);
+                          int L, float *ws_o, float *ws_ml, const DecodePlan &pl,
+                          const DecodeFuse &fz, hipStream_t st) {
+  if (D == 128) launch_decode_d<T, 128>(a, G, grid, seqlens, L, ws_o, ws_ml, pl, fz, st);
+  else launch_decode_d<T, 64>(a, G, grid, seqlens, L, ws_o, ws_ml, pl, fz, st);
 }
 
 } // namespace tpp
@@ -670,6 +800,30 @@ extern "C" size_t tpp_attn_decode_workspace_size(int64_t B, int64_t Hq, int64_t 
   return plan_decode(B, Hq, Hkv, D, Lmax).ws_bytes;
 }
 
+static int decode_impl(const char *name, AttnArgs &a, int64_t D, int64_t Lmax,
+                       const int32_t *seqlens, const DecodeFuse &fz, int dtype, void *workspace,
+                       size_t ws_bytes, void *stream) {
+  if (int e = check_attn(name, a, D)) return e;
+  if (a.B == 0) return TPP_OK;
+  if (D != 64 && D != 128)
+    return set_error(TPP_E_UNSUPPORTED, "%s: head_dim %lld not in {64, 128}", name, (long long)D);
+  if (a.Hq / a.Hkv > kDecMaxG)
+    return set_error(TPP_E_UNSUPPORTED, "%s: more than %d query heads per KV head", name,
+                     kDecMaxG);
+  if (!strides16(a)) return set_error(TPP_E_INVALID, "%s: 16-byte alignment required", name);
+  const DecodePlan pl = plan_decode(a.B, a.Hq, a.Hkv, D, Lmax);
+  if (!workspace || ws_bytes < pl.ws_bytes || !aligned16(workspace))
+    return set_error(TPP_E_WORKSPACE, "%s: workspace of %zu bytes required", name, pl.ws_bytes);
+  float *ws_o = (float *)workspace;
+  float *ws_ml = ws_o + (size_t)((int64_t)a.B * a.Hq * pl.nsplit) * D;
+  hipStream_t st = as_stream(stream);
+  const dim3 grid((unsigned)pl.nsplit, (unsigned)a.Hkv, (unsigned)a.B);
+  return TPP_DISPATCH_HALF(dtype, [&] {
+    launch_decode<T>(a, D, a.Hq / a.Hkv, grid, seqlens, (int)Lmax, ws_o, ws_ml, pl, fz, st);
+    return check_launch(name);
+  });
+}
+
 extern "C" int tpp_attn_decode(const void *q, const void *k_cache, const void *v_cache, void *o,
                                const int64_t *q_strides, const int64_t *k_strides,
                                const int64_t *v_strides, const int64_t *o_strides,
@@ -684,23 +838,34 @@ extern "C" int tpp_attn_decode(const void *q, const void *k_cache, const void *v
   AttnArgs a = make_args(q, k_cache, v_cache, o, q_strides, k_strides, v_strides, o_strides, B,
                          1, Lmax, Hq, Hkv, D, softmax_scale, window_left < 0 ? -1 : window_left,
                          0);
-  if (int e = check_attn(name, a, D)) return e;
-  if (B == 0) return TPP_OK;
-  if (D != 64 && D != 128)
-    return set_error(TPP_E_UNSUPPORTED, "%s: head_dim %lld not in {64, 128}", name, (long long)D);
-  if (Hq / Hkv > kDecMaxG)
-    return set_error(TPP_E_UNSUPPORTED, "%s: more than %d query heads per KV head", name,
-                     kDecMaxG);
-  if (!strides16(a)) return set_error(TPP_E_INVALID, "%s: 16-byte alignment required", name);
-  const DecodePlan pl = plan_decode(B, Hq, Hkv, D, Lmax);
-  if (!workspace || ws_bytes < pl.ws_bytes || !aligned16(workspace))
-    return set_error(TPP_E_WORKSPACE, "%s: workspace of %zu bytes required", name, pl.ws_bytes);
-  float *ws_o = (float *)workspace;
-  float *ws_ml = ws_o + (size_t)(B * Hq * pl.nsplit) * D;
-  hipStream_t st = as_stream(stream);
-  const dim3 grid((unsigned)pl.nsplit, (unsigned)Hkv, (unsigned)B);
-  return TPP_DISPATCH_HALF(dtype, [&] {
-    launch_decode<T>(a, D, (int)(Hq / Hkv), grid, seqlens, (int)Lmax, ws_o, ws_ml, pl, st);
-    return check_launch(name);
-  });
+  DecodeFuse fz{};
+  return decode_impl(name, a, D, Lmax, seqlens, fz, dtype, workspace, ws_bytes, stream);
+}
+
+extern "C" int tpp_attn_decode_fused(const void *qkv, const void *q_norm_w, const void *k_norm_w,
+                                     const void *cos, const void *sin, int64_t ctx, int cs_dtype,
+                                     float eps, void *k_cache, void *v_cache, void *o,
+                                     const int64_t *k_strides, const int64_t *v_strides,
+                                     const int64_t *o_strides, const int32_t *seqlens, int64_t B,
+                                     int64_t Hq, int64_t Hkv, int64_t D, int64_t Lmax,
+                                     float softmax_scale, int window_left, int dtype,
+                                     void *workspace, size_t ws_bytes, void *stream) {
+  const char *name = "tpp_attn_decode_fused";
+  if (!k_strides || !v_strides || !o_strides)
+    return set_error(TPP_E_INVALID, "%s: null stride array", name);
+  if (!qkv || !cos || !sin || !seqlens)
+    return set_error(TPP_E_INVALID, "%s: qkv, cos, sin and seqlens are required", name);
+  if (!aligned16(qkv) || !aligned16(cos) || !aligned16(sin) ||
+      (q_norm_w && !aligned16(q_norm_w)) || (k_norm_w && !aligned16(k_norm_w)))
+    return set_error(TPP_E_INVALID, "%s: 16-byte alignment required", name);
+  if (cs_dtype != TPP_F16 && cs_dtype != TPP_BF16 && cs_dtype != TPP_F32)
+    return set_error(TPP_E_UNSUPPORTED, "%s: cos/sin dtype", name);
+  if (ctx <= 0 || ctx > 0x7fffffff) return set_error(TPP_E_INVALID, "%s: ctx", name);
+  if (B > 0xffff || Hkv > 0xffff || Lmax > 0x7fffffff)
+    return set_error(TPP_E_UNSUPPORTED, "%s: dimension too large", name);
+  const int64_t qs[3] = {0, 0, 0};
+  AttnArgs a = make_args(qkv, k_cache, v_cache, o, qs, k_strides, v_strides, o_strides, B, 1,
+                         Lmax, Hq, Hkv, D, softmax_scale, window_left < 0 ? -1 : window_left, 0);
+  DecodeFuse fz{qkv, q_norm_w, k_norm_w, cos, sin, cs_dtype, (int)ctx, eps};
+  return decode_impl(name, a, D, Lmax, seqlens, fz, dtype, workspace, ws_bytes, stream);
 }

@@ -445,6 +445,41 @@ at::Tensor cached_workspace(const at::Tensor &like, size_t bytes) {
   return ws;
 }
 
+// greedy decode tail: ids <- argmax(lm_head(norm(input))), resid_next <-
+// emb[ids], positions/seqlens += 1 (all in place)
+void greedy_step(at::Tensor input, at::Tensor weight, c10::optional<at::Tensor> norm_w, double eps,
+                 at::Tensor emb, at::Tensor ids, at::Tensor resid_next,
+                 c10::optional<at::Tensor> positions, c10::optional<at::Tensor> seqlens) {
+  check_linear(input, weight);
+  const int64_t K = weight.size(1), N = weight.size(0), B = input.numel() / K;
+  check_rows16(input, K);
+  const void *nw = norm_ptr(norm_w, input, K);
+  TORCH_CHECK(emb.is_cuda() && emb.scalar_type() == input.scalar_type() && emb.dim() == 2 &&
+                  emb.size(0) == N && emb.size(1) == K && emb.is_contiguous(),
+              "emb must be a contiguous [N, K] tensor of the input dtype");
+  TORCH_CHECK(ids.is_cuda() && ids.scalar_type() == at::kLong && ids.numel() == B &&
+                  ids.is_contiguous(),
+              "ids must be a contiguous int64 tensor of B elements");
+  TORCH_CHECK(resid_next.is_cuda() && resid_next.scalar_type() == input.scalar_type() &&
+                  resid_next.numel() == B * K && resid_next.is_contiguous(),
+              "resid_next must be a contiguous [B, K] tensor of the input dtype");
+  auto i32 = [&](const c10::optional<at::Tensor> &t, const char *what) -> int32_t * {
+    if (!t.has_value() || !t->defined()) return nullptr;
+    TORCH_CHECK(t->is_cuda() && t->scalar_type() == at::kInt && t->numel() == B &&
+                    t->is_contiguous(),
+                what, " must be a contiguous int32 tensor of B elements");
+    return t->data_ptr<int32_t>();
+  };
+  int32_t *pp = i32(positions, "positions"), *sp = i32(seqlens, "seqlens");
+  c10::DeviceGuard g(input.device());
+  const size_t wsb = tpp_gemv_argmax_workspace_size(B, N);
+  auto ws = cached_workspace(input, wsb);
+  check_rc(tpp_greedy_step(input.data_ptr(), nw, (float)eps, weight.data_ptr(), emb.data_ptr(),
+                           ids.data_ptr<int64_t>(), resid_next.data_ptr(), pp, sp, B, N, K,
+                           dtype_code(input), ws.data_ptr(), wsb, cur_stream(input)),
+           "greedy_step");
+}
+
 void check_bshd(const at::Tensor &t, const char *what) {
   TORCH_CHECK(t.is_cuda(), what, " must be on CUDA");
   TORCH_CHECK(is_half_or_bf16(t), what, " must be float16 or bfloat16");
@@ -540,9 +575,56 @@ at::Tensor argmax_rows(at::Tensor x) {
   return out.view(shp);
 }
 
+// decode attention with the new token's QK-norm + RoPE + cache append fused in
+at::Tensor attn_decode_fused(at::Tensor qkv, c10::optional<at::Tensor> q_norm_w,
+                             c10::optional<at::Tensor> k_norm_w, at::Tensor cos, at::Tensor sin,
+                             double eps, at::Tensor k_cache, at::Tensor v_cache,
+                             at::Tensor seqlens, double softmax_scale, int64_t window_left) {
+  TORCH_CHECK(qkv.is_cuda() && qkv.is_contiguous() && is_half_or_bf16(qkv),
+              "qkv must be a contiguous CUDA half/bfloat16 tensor [B, 1, (Hq+2Hkv)*D]");
+  TORCH_CHECK(k_cache.is_cuda() && v_cache.is_cuda() && k_cache.dim() == 4 &&
+                  k_cache.sizes() == v_cache.sizes() && k_cache.stride(3) == 1 &&
+                  v_cache.stride(3) == 1 && k_cache.scalar_type() == qkv.scalar_type() &&
+                  v_cache.scalar_type() == qkv.scalar_type(),
+              "caches must be CUDA [B, Hkv, Lmax, D] of the qkv dtype");
+  const int64_t B = k_cache.size(0), Hkv = k_cache.size(1), Lmax = k_cache.size(2),
+                D = k_cache.size(3);
+  TORCH_CHECK(qkv.numel() % (B * D) == 0, "qkv size mismatch");
+  const int64_t Hq = qkv.numel() / (B * D) - 2 * Hkv;
+  TORCH_CHECK(Hq > 0 && Hq % Hkv == 0, "qkv size does not give a valid head count");
+  TORCH_CHECK(seqlens.is_cuda() && seqlens.scalar_type() == at::kInt && seqlens.numel() == B &&
+                  seqlens.is_contiguous(),
+              "seqlens must be a contiguous CUDA int32 tensor [B]");
+  TORCH_CHECK(cos.is_contiguous() && sin.is_contiguous() && cos.dim() == 2 && cos.size(1) == D &&
+                  sin.sizes() == cos.sizes() && sin.scalar_type() == cos.scalar_type() &&
+                  dtype_code(cos) >= 0,
+              "cos/sin must be contiguous [ctx, D] tables");
+  const void *qw = norm_ptr(q_norm_w, qkv, D), *kw = norm_ptr(k_norm_w, qkv, D);
+  c10::DeviceGuard g(qkv.device());
+  auto o = torch::empty({B, 1, Hq, D}, qkv.options());
+  const size_t wsb = tpp_attn_decode_workspace_size(B, Hq, Hkv, D, Lmax);
+  at::Tensor ws = cached_workspace(qkv, wsb);
+  const int64_t ks[3] = {k_cache.stride(0), k_cache.stride(2), k_cache.stride(1)};
+  const int64_t vs[3] = {v_cache.stride(0), v_cache.stride(2), v_cache.stride(1)};
+  const int64_t os[3] = {o.stride(0), o.stride(1), o.stride(2)};
+  check_rc(tpp_attn_decode_fused(qkv.data_ptr(), qw, kw, cos.data_ptr(), sin.data_ptr(),
+                                 cos.size(0), dtype_code(cos), (float)eps, k_cache.data_ptr(),
+                                 v_cache.data_ptr(), o.data_ptr(), ks, vs, os,
+                                 seqlens.data_ptr<int32_t>(), B, Hq, Hkv, D, Lmax,
+                                 (float)softmax_scale, (int)window_left, dtype_code(qkv),
+                                 ws.data_ptr(), (size_t)ws.numel() * 4, cur_stream(qkv)),
+           "attn_decode_fused");
+  return o;
+}
+
 } // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("attn_decode_fused", &attn_decode_fused,
+        "decode attention with QK-norm + RoPE + KV append of the new token fused in",
+        py::arg("qkv"), py::arg("q_norm_w"), py::arg("k_norm_w"), py::arg("cos"), py::arg("sin"),
+        py::arg("eps"), py::arg("k_cache"), py::arg("v_cache"), py::arg("seqlens"),
+        py::arg("softmax_scale") = 0.0, py::arg("window_left") = -1);
   m.def("argmax_rows", &argmax_rows, "argmax over the last dim (greedy sampling)", py::arg("x"));
   m.def("flash_attn_func", &attn_fwd, "flash attention forward (GQA, causal, window)",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("causal") = false,
@@ -584,6 +666,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gemv_argmax", &gemv_argmax, "lm_head GEMV fused with greedy argmax", py::arg("input"),
         py::arg("weight"), py::arg("norm_weight") = py::none(), py::arg("eps") = 1e-6,
         py::arg("return_logits") = false);
+  m.def("greedy_step", &greedy_step,
+        "greedy decode tail: argmax(lm_head) -> ids, embedding gather, position advance",
+        py::arg("input"), py::arg("weight"), py::arg("norm_weight"), py::arg("eps"),
+        py::arg("emb"), py::arg("ids"), py::arg("resid_next"),
+        py::arg("positions") = py::none(), py::arg("seqlens") = py::none());
   m.doc() = "torchpp gfx950 kernel set (binding over libtorchpp_hip.so)";
   m.def("rmsnormFused", &rmsnorm_fused, "Fused RMSNorm (fp16/bf16)", py::arg("input"),
         py::arg("weight"), py::arg("eps") = 1e-6);

@@ -155,48 +155,49 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   };
   if (x_res) load_x(k_begin, xa);
 
-  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    int64_t row0, row1 = 0;
+  // per-block running argmax over all tiles (wave 0, lanes r == 0 hold it)
+  float am_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  int am_i[4] = {0x7fffffff, 0x7fffffff, 0x7fffffff, 0x7fffffff};
+
+  auto rows_of = [&](int64_t tile, int64_t &row0, int64_t &row1) {
     if constexpr (EPI == kEpiSwiGLU) {
       row0 = (tile >> 1) * 64 + (tile & 1) * 16;
       row1 = row0 + 32;
     } else {
       row0 = tile * 16;
+      row1 = 0;
     }
+  };
+  // W of one tile for this wave's K batch at k, plus the residual values
+  // the tile will update
+  auto load_w = [&](int64_t tile, int64_t k, V8 (&b0)[NS], V8 (&b1)[NS], float (&res)[4]) {
+    int64_t row0, row1;
+    rows_of(tile, row0, row1);
     const bool w0ok = row0 + r < N;
     const T *w0 = W + (w0ok ? row0 + r : 0) * K;
     const bool w1ok = (EPI == kEpiSwiGLU) && (row1 + r < N);
     const T *w1 = W + (w1ok ? row1 + r : 0) * K;
-    // residual values this tile will update: fetched with the weights
-    float res_in[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int64_t c = k + u * 32 + g * 8;
+      const bool in = c < k_end;
+      b0[u] = ld16(w0 + c, in && w0ok);
+      if constexpr (EPI == kEpiSwiGLU) b1[u] = ld16(w1 + c, in && w1ok);
+    }
     if constexpr (EPI == kEpiResidual) {
       if (w == 0 && row0 + r < N) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int b = 4 * g + i;
-          if (b < a.NB) res_in[i] = to_f32(((const T *)a.residual)[(int64_t)b * a.ldy + row0 + r]);
+          if (b < a.NB) res[i] = to_f32(((const T *)a.residual)[(int64_t)b * a.ldy + row0 + r]);
         }
       }
     }
-    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t k = k_begin; k < k_end; k += kGemvWaveK) {
-      V8 b0[NS], b1[NS];
-#pragma unroll
-      for (int u = 0; u < NS; ++u) {
-        const int64_t c = k + u * 32 + g * 8;
-        const bool in = c < k_end;
-        b0[u] = ld16(w0 + c, in && w0ok);
-        if constexpr (EPI == kEpiSwiGLU) b1[u] = ld16(w1 + c, in && w1ok);
-      }
-      V8 xl[NS];
-      if (!x_res) load_x(k, xl);
-#pragma unroll
-      for (int u = 0; u < NS; ++u) {
-        const V8 xv = x_res ? xa[u] : xl[u];
-        acc0 = mfma16<T>(xv, b0[u], acc0);
-        if constexpr (EPI == kEpiSwiGLU) acc1 = mfma16<T>(xv, b1[u], acc1);
-      }
-    }
+  };
+  // block-wide K reduction of a tile's accumulators and its epilogue
+  auto finish = [&](int64_t tile, f32x4 acc0, f32x4 acc1, const float (&res_in)[4]) {
+    int64_t row0, row1;
+    rows_of(tile, row0, row1);
     red[0][w][lane] = acc0;
     if constexpr (EPI == kEpiSwiGLU) red[1][w][lane] = acc1;
     __syncthreads();
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       // D layout of 16x16x32: lane -> column r (weight row), rows b = 4g + i.
       const int64_t n0 = row0 + r, n1 = row1 + r;
       T *Y = (T *)a.y;
-      if (a.am_val) { // argmax partials over this tile's 16 columns
+      if (a.am_val) { // running argmax over this block's columns
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float bv = n0 < N ? to_f32(from_f32<T>(acc0[i])) : -INFINITY;
@@ -221,11 +222,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
             const int oi = __shfl_xor(bix, sh, kWave);
             if (am_better(ov, oi, bv, bix)) bv = ov, bix = oi;
           }
-          const int b = 4 * g + i;
-          if (r == 0 && b < a.NB) {
-            a.am_val[tile * a.NB + b] = bv;
-            a.am_idx[tile * a.NB + b] = bix;
-          }
+          if (am_better(bv, bix, am_v[i], am_i[i])) am_v[i] = bv, am_i[i] = bix;
         }
       }
 #pragma unroll
@@ -250,6 +247,58 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       }
     }
     __syncthreads(); // red[] is reused by the next tile
+  };
+  auto mfma_batch = [&](const V8 (&xv)[NS], const V8 (&b0)[NS], const V8 (&b1)[NS], f32x4 &acc0,
+                        f32x4 &acc1) {
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      acc0 = mfma16<T>(xv[u], b0[u], acc0);
+      if constexpr (EPI == kEpiSwiGLU) acc1 = mfma16<T>(xv[u], b1[u], acc1);
+    }
+  };
+
+  const int64_t stride = gridDim.x;
+  if (x_res) {
+    // one K batch per wave: keep two tiles in flight (W of tile t + stride is
+    // requested before tile t is reduced and written)
+    V8 pa0[NS], pa1[NS], pb0[NS], pb1[NS];
+    float ra[4] = {0.f, 0.f, 0.f, 0.f}, rb[4] = {0.f, 0.f, 0.f, 0.f};
+    int64_t t = blockIdx.x;
+    if (t < tiles) load_w(t, k_begin, pa0, pa1, ra);
+    for (; t < tiles; t += 2 * stride) {
+      const int64_t t2 = t + stride;
+      if (t2 < tiles) load_w(t2, k_begin, pb0, pb1, rb);
+      f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+      mfma_batch(xa, pa0, pa1, c0, c1);
+      finish(t, c0, c1, ra);
+      if (t2 >= tiles) break;
+      if (t2 + stride < tiles) load_w(t2 + stride, k_begin, pa0, pa1, ra);
+      f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+      mfma_batch(xa, pb0, pb1, d0, d1);
+      finish(t2, d0, d1, rb);
+    }
+  } else {
+    for (int64_t tile = blockIdx.x; tile < tiles; tile += stride) {
+      f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+      float res[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int64_t k = k_begin; k < k_end; k += kGemvWaveK) {
+        V8 b0[NS], b1[NS], xl[NS];
+        load_w(tile, k, b0, b1, res);
+        load_x(k, xl);
+        mfma_batch(xl, b0, b1, c0, c1);
+      }
+      finish(tile, c0, c1, res);
+    }
+  }
+  if (a.am_val && w == 0 && r == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = 4 * g + i;
+      if (b < a.NB) {
+        a.am_val[(int64_t)blockIdx.x * a.NB + b] = am_v[i];
+        a.am_idx[(int64_t)blockIdx.x * a.NB + b] = am_i[i];
+      }
+    }
   }
 }
 
@@ -297,17 +346,15 @@ __global__ __launch_bounds__(256) void gemv_scalar_kernel(GemvArgs a, int64_t NO
   }
 }
 
-// Final reduction of the argmax partials: out[b] = best over tiles.
-__global__ __launch_bounds__(1024) void argmax_partials_kernel(const float *__restrict__ val,
-                                                               const int *__restrict__ idx,
-                                                               int tiles, int NB,
-                                                               int64_t *__restrict__ out) {
+// Final reduction of the per-block argmax partials of row b; block = 1024.
+__device__ __forceinline__ int argmax_finish(const float *__restrict__ val,
+                                             const int *__restrict__ idx, int nparts, int NB,
+                                             int b) {
   __shared__ float sv[16];
   __shared__ int si[16];
-  const int b = blockIdx.x;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int t = threadIdx.x; t < tiles; t += blockDim.x) {
+  for (int t = threadIdx.x; t < nparts; t += blockDim.x) {
     const float v = val[(int64_t)t * NB + b];
     const int i = idx[(int64_t)t * NB + b];
     if (am_better(v, i, bv, bi)) bv = v, bi = i;
@@ -326,8 +373,37 @@ __global__ __launch_bounds__(1024) void argmax_partials_kernel(const float *__re
   if (threadIdx.x == 0) {
     for (int w = 1; w < (int)(blockDim.x / kWave); ++w)
       if (am_better(sv[w], si[w], bv, bi)) bv = sv[w], bi = si[w];
-    out[b] = bi;
+    si[0] = bi;
   }
+  __syncthreads();
+  return si[0];
+}
+
+__global__ __launch_bounds__(1024) void argmax_partials_kernel(const float *__restrict__ val,
+                                                               const int *__restrict__ idx,
+                                                               int nparts, int NB,
+                                                               int64_t *__restrict__ out) {
+  const int tok = argmax_finish(val, idx, nparts, NB, blockIdx.x);
+  if (threadIdx.x == 0) out[blockIdx.x] = tok;
+}
+
+// Greedy decode step epilogue: token = argmax; ids[b] = token; the next
+// step's residual row <- embedding[token]; positions[b]++, seqlens[b]++.
+template <typename T>
+__global__ __launch_bounds__(1024) void greedy_advance_kernel(
+    const float *__restrict__ val, const int *__restrict__ idx, int nparts, int NB,
+    const T *__restrict__ emb, int64_t E, int64_t *__restrict__ ids, T *__restrict__ resid,
+    int *__restrict__ positions, int *__restrict__ seqlens) {
+  const int b = blockIdx.x;
+  const int tok = argmax_finish(val, idx, nparts, NB, b);
+  if (threadIdx.x == 0) {
+    ids[b] = tok;
+    if (positions) positions[b] += 1;
+    if (seqlens) seqlens[b] += 1;
+  }
+  const T *src = emb + (int64_t)tok * E;
+  T *dst = resid + (int64_t)b * E;
+  for (int64_t e = threadIdx.x; e < E; e += blockDim.x) dst[e] = src[e];
 }
 
 static bool gemv_vec_ok(const GemvArgs &a) {
@@ -442,28 +518,63 @@ extern "C" int tpp_gemv_fused(const void *x, const void *norm_w, float eps, cons
 }
 
 extern "C" size_t tpp_gemv_argmax_workspace_size(int64_t B, int64_t N) {
-  return (size_t)((N + 15) / 16) * (size_t)B * 8;
+  const int64_t tiles = (N + 15) / 16;
+  return (size_t)(tiles < kGemvMaxBlocks ? tiles : kGemvMaxBlocks) * (size_t)B * 8;
+}
+
+static int gemv_argmax_launch(const char *name, const void *x, const void *norm_w, float eps,
+                              const void *W, void *logits, int64_t B, int64_t N, int64_t K,
+                              int dtype, void *workspace, size_t ws_bytes, hipStream_t st,
+                              GemvArgs &a, int &nparts) {
+  if (int e = gemv_args(name, x, W, B, N, K, K)) return e;
+  if (N > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: N too large", name);
+  const int64_t tiles = (N + 15) / 16;
+  nparts = (int)(tiles < kGemvMaxBlocks ? tiles : kGemvMaxBlocks);
+  const size_t need = tpp_gemv_argmax_workspace_size(B, N);
+  if (!workspace || ws_bytes < need || !aligned16(workspace))
+    return set_error(TPP_E_WORKSPACE, "%s: workspace of %zu bytes required", name, need);
+  a = make_gemv(x, K, B, norm_w, eps, W, N, K, logits, N);
+  a.am_val = (float *)workspace;
+  a.am_idx = (int *)((char *)workspace + (size_t)nparts * B * 4);
+  if (!gemv_vec_ok(a)) return set_error(TPP_E_UNSUPPORTED, "%s: needs K %% 8 == 0 and 16-byte alignment", name);
+  return TPP_DISPATCH_HALF(dtype, [&] {
+    return launch_gemv_n<T, kEpiPlain, TPP_ACT_NONE>(a, st, name);
+  });
 }
 
 extern "C" int tpp_gemv_argmax(const void *x, const void *norm_w, float eps, const void *W,
                                void *logits, int64_t *out_idx, int64_t B, int64_t N, int64_t K,
                                int dtype, void *workspace, size_t ws_bytes, void *stream) {
   const char *name = "tpp_gemv_argmax";
-  if (int e = gemv_args(name, x, W, B, N, K, K)) return e;
   if (!out_idx) return set_error(TPP_E_INVALID, "%s: null index output", name);
-  if (N > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: N too large", name);
-  const int64_t tiles = (N + 15) / 16;
-  const size_t need = tpp_gemv_argmax_workspace_size(B, N);
-  if (!workspace || ws_bytes < need || !aligned16(workspace))
-    return set_error(TPP_E_WORKSPACE, "%s: workspace of %zu bytes required", name, need);
-  GemvArgs a = make_gemv(x, K, B, norm_w, eps, W, N, K, logits, N);
-  a.am_val = (float *)workspace;
-  a.am_idx = (int *)((char *)workspace + (size_t)tiles * B * 4);
   hipStream_t st = as_stream(stream);
+  GemvArgs a;
+  int nparts = 0;
+  if (int e = gemv_argmax_launch(name, x, norm_w, eps, W, logits, B, N, K, dtype, workspace,
+                                 ws_bytes, st, a, nparts))
+    return e;
+  argmax_partials_kernel<<<dim3((unsigned)B), dim3(1024), 0, st>>>(a.am_val, a.am_idx, nparts,
+                                                                   (int)B, out_idx);
+  return check_launch(name);
+}
+
+extern "C" int tpp_greedy_step(const void *x, const void *norm_w, float eps, const void *W,
+                               const void *emb, int64_t *ids, void *resid_next,
+                               int32_t *positions, int32_t *seqlens, int64_t B, int64_t N,
+                               int64_t K, int dtype, void *workspace, size_t ws_bytes,
+                               void *stream) {
+  const char *name = "tpp_greedy_step";
+  if (!emb || !ids || !resid_next) return set_error(TPP_E_INVALID, "%s: null pointer", name);
+  hipStream_t st = as_stream(stream);
+  GemvArgs a;
+  int nparts = 0;
+  if (int e = gemv_argmax_launch(name, x, norm_w, eps, W, nullptr, B, N, K, dtype, workspace,
+                                 ws_bytes, st, a, nparts))
+    return e;
   return TPP_DISPATCH_HALF(dtype, [&] {
-    if (int e = launch_gemv_n<T, kEpiPlain, TPP_ACT_NONE>(a, st, name)) return e;
-    argmax_partials_kernel<<<dim3((unsigned)B), dim3(1024), 0, st>>>(a.am_val, a.am_idx,
-                                                                     (int)tiles, (int)B, out_idx);
+    greedy_advance_kernel<T><<<dim3((unsigned)B), dim3(1024), 0, st>>>(
+        a.am_val, a.am_idx, nparts, (int)B, (const T *)emb, K, ids, (T *)resid_next, positions,
+        seqlens);
     return check_launch(name);
   });
 }

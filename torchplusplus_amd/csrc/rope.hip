@@ -16,21 +16,6 @@
 
 namespace tpp {
 
-template <typename CS>
-__device__ __forceinline__ void load_cs8(const CS *p, float (&v)[8]) {
-  if constexpr (sizeof(CS) == 4) {
-    f32x4 a = *reinterpret_cast<const f32x4 *>(p);
-    f32x4 b = *reinterpret_cast<const f32x4 *>(p + 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = a[i];
-      v[i + 4] = b[i];
-    }
-  } else {
-    load8(p, v);
-  }
-}
-
 __device__ __forceinline__ void rotate8(float (&x1)[8], float (&x2)[8], const float (&c1)[8],
                                         const float (&c2)[8], const float (&s1)[8],
                                         const float (&s2)[8]) {
@@ -163,14 +148,6 @@ static int rope_dispatch(const void *q, void *qo, int64_t rows_q, const void *k,
 // One 16-byte chunk of each half-row per lane, D/16 lanes per row, the row
 // RMS reduced with DPP inside those lanes.
 // ---------------------------------------------------------------------------
-template <int LPR> __device__ __forceinline__ float group_sum(float v) {
-  v += dpp_f32<kDppQuadXor1>(v);
-  if constexpr (LPR >= 4) v += dpp_f32<kDppQuadXor2>(v);
-  if constexpr (LPR >= 8) v += dpp_f32<kDppRowHalfMirror>(v);
-  if constexpr (LPR >= 16) v += dpp_f32<kDppRowMirror>(v);
-  return v;
-}
-
 template <typename T, typename CS, int LPR>
 __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
     const T *__restrict__ qkv, T *__restrict__ q_out, T *__restrict__ k_cache,

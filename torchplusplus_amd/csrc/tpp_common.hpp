@@ -120,6 +120,39 @@ __device__ __forceinline__ float xor_sum(float v, int mask) {
   return v + __shfl_xor(v, mask, kWave);
 }
 
+// Sum over aligned groups of LPR lanes (LPR in {2, 4, 8, 16}) with DPP.
+template <int LPR> __device__ __forceinline__ float group_sum(float v) {
+  v += dpp_f32<kDppQuadXor1>(v);
+  if constexpr (LPR >= 4) v += dpp_f32<kDppQuadXor2>(v);
+  if constexpr (LPR >= 8) v += dpp_f32<kDppRowHalfMirror>(v);
+  if constexpr (LPR >= 16) v += dpp_f32<kDppRowMirror>(v);
+  return v;
+}
+
+// 8 consecutive RoPE table entries of type CS (fp16, bf16 or fp32) as fp32.
+template <typename CS>
+__device__ __forceinline__ void load_cs8(const CS *p, float (&v)[8]) {
+  if constexpr (sizeof(CS) == 4) {
+    f32x4 a = *reinterpret_cast<const f32x4 *>(p);
+    f32x4 b = *reinterpret_cast<const f32x4 *>(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[i + 4] = b[i];
+    }
+  } else {
+    load8(p, v);
+  }
+}
+
+// Same with the table type chosen at run time (a tpp_dtype code).
+__device__ __forceinline__ void load_cs8_rt(const void *p, int64_t idx, int cs_dtype,
+                                            float (&v)[8]) {
+  if (cs_dtype == TPP_F32) load_cs8((const float *)p + idx, v);
+  else if (cs_dtype == TPP_F16) load_cs8((const f16 *)p + idx, v);
+  else load_cs8((const bf16 *)p + idx, v);
+}
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
 

@@ -10,10 +10,11 @@ it intends, down(silu(gate(x)) * up(x)) (the committed FFN feeds the
 Execution:
   * forward_impl keeps the residual stream in one buffer. For prefill it
     fuses each residual add into the next RMSNorm; for <= 16 tokens
-    (decode) each RMSNorm is fused into the GEMV that reads it and each
-    residual add into the GEMV that writes it, so a layer is 6 kernels:
-    QKV GEMV, QK-norm+RoPE+KV-append, split-KV attention (+combine), o_proj
-    GEMV, SwiGLU GEMV, down GEMV.
+    (decode) each RMSNorm is fused into the GEMV that reads it, each
+    residual add into the GEMV that writes it, and the QK-norm + RoPE +
+    KV-append of the new token into the decode attention kernel, so a layer
+    is 6 kernels: QKV GEMV, split-KV attention (+merge), o_proj GEMV, SwiGLU
+    GEMV, down GEMV.
   * GreedyDecoder captures one whole decode step (28 layers, lm_head,
     argmax, position advance) into a HIP graph and replays it per token, so
     the token loop issues one launch per token and never synchronises.
@@ -197,15 +198,18 @@ class FastQwen3(LLMInference):
 class GreedyDecoder:
     """One greedy decode step for every sequence of the batch, on static
     buffers so it can be captured in a HIP graph:
-      ids [B, 1] (current token) -> 28 blocks (GEMV projections, fused
-      QK-norm/RoPE/KV append at `positions`, split-KV attention over
-      `seqlens` keys) -> lm_head GEMV -> argmax -> ids; positions += 1."""
+      resid [B, 1, E] (embedding of the current token) -> 28 blocks (GEMV
+      projections, fused QK-norm/RoPE/KV append at `positions`, split-KV
+      attention over `seqlens` keys) -> lm_head GEMV + argmax -> ids, and the
+      next token's embedding gathered into resid; positions, seqlens += 1."""
 
     def __init__(self, model: FastQwen3, batch_size: int):
         self.m = model
         self.B = batch_size
         dev = model.out_head.weight.device
+        emb = model.tok_embed.weight
         self.ids = torch.zeros(batch_size, 1, dtype=torch.long, device=dev)
+        self.resid = torch.zeros(batch_size, 1, emb.shape[1], dtype=emb.dtype, device=dev)
         self.positions = torch.zeros(batch_size, dtype=torch.int32, device=dev)
         self.seqlens = torch.zeros(batch_size, dtype=torch.int32, device=dev)
         self.graph = None
@@ -213,25 +217,22 @@ class GreedyDecoder:
         assert self.caches is not None, "setup_kv_cache() first"
 
     def step(self):
-        m, B = self.m, self.B
-        resid = F.embedding(self.ids, m.tok_embed.weight)  # [B, 1, E], updated in place
+        m, B, resid = self.m, self.B, self.resid
         for i, blk in enumerate(m.transformer_blocs):
             at, n1, n2 = blk.attn, blk.rms_norm1, blk.rms_norm2
             kc, vc = self.caches[i].k_cache, self.caches[i].v_cache
             qkv = _C.gemv_fused(resid, at.fused_qkv_weight(), n1.weight, n1.eps)
-            q = at.rope_cache(qkv, m.cos, m.sin, kc, vc, self.positions)
-            o = _C.attn_decode(q, kc, vc, self.seqlens, 0.0, -1, None)
+            o = at.decode_fused(qkv, m.cos, m.sin, kc, vc, self.seqlens)
             _C.gemv_fused(o.view(B, 1, at.d_out), at.out_projection.weight, None, 1e-6, resid)
             h = _C.gemv_swiglu(resid, blk.ffn.w_gu(), n2.weight, n2.eps)
             _C.gemv_fused(h, blk.ffn.linear_layer2.weight, None, 1e-6, resid)
         fn = m.final_rmsnorm
-        tok = _C.gemv_argmax(resid, m.out_head.weight, fn.weight, fn.eps, False)[0]
-        self.ids.copy_(tok.view(B, 1))
-        self.positions.add_(1)
-        self.seqlens.add_(1)
+        _C.greedy_step(resid, m.out_head.weight, fn.weight, fn.eps, m.tok_embed.weight,
+                       self.ids, resid, self.positions, self.seqlens)
 
     def prepare(self, first_tokens: torch.Tensor, position: int):
         self.ids.copy_(first_tokens.view(self.B, 1))
+        self.resid.copy_(F.embedding(self.ids, self.m.tok_embed.weight))
         self.positions.fill_(position)
         self.seqlens.fill_(position + 1)
         for c in self.caches:
@@ -239,15 +240,17 @@ class GreedyDecoder:
 
     def capture(self):
         """Warm up once on a side stream, restore the state, then capture."""
-        saved = (self.ids.clone(), self.positions.clone(), self.seqlens.clone())
+        saved = (self.ids.clone(), self.resid.clone(), self.positions.clone(),
+                 self.seqlens.clone())
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             self.step()
         torch.cuda.current_stream().wait_stream(s)
         self.ids.copy_(saved[0])
-        self.positions.copy_(saved[1])
-        self.seqlens.copy_(saved[2])
+        self.resid.copy_(saved[1])
+        self.positions.copy_(saved[2])
+        self.seqlens.copy_(saved[3])
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self.step()
