@@ -166,6 +166,128 @@ def measure_kernels(model, dec, cfg, L):
     return out, attn_us, attn_bytes
 
 
+def _rotating(make, n):
+    """n independent argument sets (make(i)) and a call counter: a graph of n
+    launches touches n distinct buffer sets (cold: > 2x the 256 MB MALL when
+    n * bytes > 512 MB), or the first set n times (warm)."""
+    sets = [make(i) for i in range(n)]
+    it = {"i": 0}
+
+    def nxt(cold):
+        if not cold:
+            return sets[0]
+        it["i"] = (it["i"] + 1) % n
+        return sets[it["i"]]
+    return nxt
+
+
+def _cold_warm(call, nxt, n):
+    keep = []  # outputs stay alive, so each captured launch writes its own buffer
+    cold = event_time_us(lambda: keep.append(call(*nxt(True))), n)
+    keep.clear()
+    warm = event_time_us(lambda: call(*nxt(False)), n)
+    return cold, warm
+
+
+def _cfg_entry(cfg_idx, name, bound, cold, warm, amount):
+    e = (hbm_entry if bound == "hbm" else mfma_entry)(name, cold, amount)
+    w = (hbm_entry if bound == "hbm" else mfma_entry)(name, warm, amount)
+    e["config"] = cfg_idx
+    e["us_warm"] = w["us"]
+    e["frac_warm"] = w["frac"]
+    return e
+
+
+def measure_configs():
+    """BASELINE.json configs[0..3] at their stated shapes, dtypes and
+    distributions (seeded). HBM-bound ops rotate through >= 512 MB of
+    distinct buffers for the cold figure; `us_warm` repeats one buffer set."""
+    from torchplusplus_amd._native import ext
+    from torchplusplus_amd.dlops.rope import compute_rope_params
+
+    C = ext()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    out = []
+
+    def randn(*shape, dtype, std=1.0, mean=0.0):
+        return (mean + std * torch.randn(*shape, generator=g, device=dev, dtype=torch.float32)).to(dtype)
+
+    # configs[0]: RMSNorm fp16 [4096, 1024]
+    M, N = 4096, 1024
+    w = randn(N, dtype=torch.float16, std=0.1, mean=1.0)
+    nxt = _rotating(lambda i: (randn(M, N, dtype=torch.float16),), 40)
+    cold, warm = _cold_warm(lambda x: C.rmsnormFused(x, w, 1e-6), nxt, 40)
+    out.append(_cfg_entry(0, "rmsnormFused fp16 [4096x1024]", "hbm", cold, warm, 2 * M * N * 2 + N * 2))
+    # LayerNorm has no config of its own; same shape
+    cold, warm = _cold_warm(lambda x: C.applyLayernorm(x, w, 1e-6), nxt, 40)
+    out.append(_cfg_entry(0, "applyLayernorm fp16 [4096x1024]", "hbm", cold, warm, 2 * M * N * 2 + N * 2))
+    del nxt
+
+    # configs[1]: RoPE on Q [1,16,2048,128], K [1,8,2048,128] bf16, theta 1e6
+    S, D = 2048, 128
+    cos, sin = compute_rope_params(D, 1e6, S, device=dev, out_dtype=torch.bfloat16)
+    nxt = _rotating(lambda i: (randn(1, 16, S, D, dtype=torch.bfloat16),
+                               randn(1, 8, S, D, dtype=torch.bfloat16)), 24)
+    rope_bytes = 2 * (16 + 8) * S * D * 2 + 2 * S * D * 2
+    cold, warm = _cold_warm(lambda q, k: C.qkrope_apply_cuda(q, k, cos, sin), nxt, 24)
+    out.append(_cfg_entry(1, "qkrope_apply Q[1,16,2048,128] K[1,8,2048,128] bf16", "hbm", cold, warm,
+                          rope_bytes))
+
+    def inplace(q, k):
+        C.rope_apply_(q, cos, sin)
+        C.rope_apply_(k, cos, sin)
+    cold, warm = _cold_warm(inplace, nxt, 24)
+    out.append(_cfg_entry(1, "rope_apply_ (in place, 2 launches) Q+K bf16", "hbm", cold, warm, rope_bytes))
+    del nxt
+    # configs[1]: Linear+SiLU bf16 [2048x1024] @ [1024x3072] + bias
+    M, K, N = 2048, 1024, 3072
+    nxt = _rotating(lambda i: (randn(M, K, dtype=torch.bfloat16), randn(N, K, dtype=torch.bfloat16, std=0.02),
+                               randn(N, dtype=torch.bfloat16, std=0.02)), 24)
+    cold, warm = _cold_warm(lambda x, W, b: C.LinearSilu(x, W, b), nxt, 24)
+    out.append(_cfg_entry(1, "LinearSilu bf16 [2048x1024]x[3072x1024]^T +bias", "mfma", cold, warm,
+                          2 * M * N * K))
+    cold, warm = _cold_warm(lambda x, W, b: C.LinearGelu(x, W, b), nxt, 24)
+    out.append(_cfg_entry(1, "LinearGelu bf16 [2048x1024]x[3072x1024]^T +bias", "mfma", cold, warm,
+                          2 * M * N * K))
+    del nxt
+
+    # configs[2]: prefill B4 S2048 16/8 d128 causal, and window 512
+    B, S, Hq, Hkv = 4, 2048, 16, 8
+    q = randn(B, S, Hq, D, dtype=torch.bfloat16)
+    k = randn(B, S, Hkv, D, dtype=torch.bfloat16)
+    v = randn(B, S, Hkv, D, dtype=torch.bfloat16)
+    t = event_time_us(lambda: C.flash_attn_func(q, k, v, True, -1, -1, 0.0), 8)
+    out.append(_cfg_entry(2, "flash_attn causal B4 S2048 16/8 d128", "mfma", t, t,
+                          4 * B * Hq * D * (S * (S + 1) // 2)))
+    keys = sum(min(i + 1, 512) for i in range(S))
+    t = event_time_us(lambda: C.flash_attn_func(q, k, v, True, 511, 0, 0.0), 8)
+    out.append(_cfg_entry(2, "flash_attn causal window 512 B4 S2048 16/8 d128", "mfma", t, t,
+                          4 * B * Hq * D * keys))
+    del q, k, v
+
+    # configs[3]: hgemv fp16 [1x1024]@[1024x3072] and [1x3072]@[3072x1024]
+    for (Mo, K) in ((3072, 1024), (1024, 3072)):
+        nxt = _rotating(lambda i: (randn(1, K, dtype=torch.float16),
+                                   randn(Mo, K, dtype=torch.float16, std=0.02)), 96)
+        cold, warm = _cold_warm(lambda x, W: C.gemv(x, W, None, 0), nxt, 96)
+        out.append(_cfg_entry(3, f"hgemv fp16 [1x{K}]x[{Mo}x{K}]^T", "hbm", cold, warm,
+                              (Mo * K + K + Mo) * 2))
+        del nxt
+    # configs[3]: decode attention B32 16/8 d128, cache 4096, bf16 ~N(0,1)
+    B, L = 32, 4096
+    kc = randn(B, Hkv, L, D, dtype=torch.bfloat16)
+    vc = randn(B, Hkv, L, D, dtype=torch.bfloat16)
+    q = randn(B, 1, Hq, D, dtype=torch.bfloat16)
+    seq = torch.full((B,), L, dtype=torch.int32, device=dev)
+    o = torch.empty_like(q)
+    t = event_time_us(lambda: C.attn_decode(q, kc, vc, seq, 0.0, -1, o), 8)
+    out.append(_cfg_entry(3, "attn_decode B32 16/8 d128 L4096 (+merge)", "hbm", t, t,
+                          2 * B * Hkv * L * D * 2 + 2 * B * Hq * D * 2))
+    del kc, vc
+    return out
+
+
 def cpu_baseline(model, cfg, steps: int = 3):
     """The oracle's eager PyTorch decode (fp32 math, bf16 rounding at op
     boundaries) on this host: batch 8, synthetic 2048-position cache."""
@@ -188,6 +310,37 @@ def cpu_baseline(model, cfg, steps: int = 3):
                       f"(random K/V), after 1 warm-up step; oracle/qwen3.py on the host CPU"}
 
 
+def traffic_probe(L: int, launches: int = 16):
+    """Counter run (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): the
+    roofline kernel at the decode-bench shape (B 8, 16/8 heads, d 128, cache
+    length L) over 8 distinct cache sets (> 512 MB, so reads come from HBM),
+    and a plain 512 MiB device copy whose counter reading calibrates KiB per
+    dispatch against known bytes."""
+    from torchplusplus_amd._native import ext
+
+    C = ext()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(3)
+    B, H, Hkv, D = BATCH, 16, 8, 128
+    sets = [(torch.randn(B, Hkv, L, D, generator=g, device=dev).bfloat16(),
+             torch.randn(B, Hkv, L, D, generator=g, device=dev).bfloat16()) for _ in range(8)]
+    q = torch.randn(B, 1, H, D, generator=g, device=dev).bfloat16()
+    seq = torch.full((B,), L, dtype=torch.int32, device=dev)
+    o = torch.empty_like(q)
+    src = torch.randn(256 << 20, generator=g, device=dev).bfloat16()  # 512 MiB
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for i in range(launches):
+        kc, vc = sets[i % 8]
+        C.attn_decode(q, kc, vc, seq, 0.0, -1, o)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "attn_decode", "B": B, "L": L, "launches": launches,
+                      "algorithmic_bytes": 2 * B * Hkv * L * D * 2 + 2 * B * H * D * 2,
+                      "copy_bytes_each_way": src.numel() * 2}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -195,11 +348,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the roofline kernel + a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the decode path shards by KV head "
               "across GPUs by design, see DESIGN.md); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.traffic_probe:
+        torch.cuda.set_device(0)
+        with torch.inference_mode():
+            traffic_probe(PREFILL + args.steps // 2)
+        return
 
     from torchplusplus_amd.fastqwen3 import FastQwen3, GreedyDecoder, QwenConfig
 
@@ -247,6 +408,8 @@ def main():
         L = PREFILL + K // 2  # mean cache length over the timed steps
         kernels, attn_us, attn_bytes = measure_kernels(model, dec, cfg, L)
         log("[bench] kernel table done")
+        configs = measure_configs()
+        log("[bench] config table done")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -277,6 +440,7 @@ def main():
                      "cache_len": L},
         "prefill": {"ms": round(prefill_s * 1e3, 3), "tok_per_s": round(BATCH * PREFILL / prefill_s, 1)},
         "kernels": kernels,
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -35,6 +35,33 @@ def test_linear_act_shapes(dev, act, m, n, k):
     close(y, oracle.linear_act(x, w, b, act), what=f"linear {act} {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("act", ["none", "gelu"])
+@pytest.mark.parametrize("m,n", [(1100, 4100), (4096, 1100), (2048, 4096)])
+def test_linear_pipelined_path_edges(dev, act, m, n):
+    """Large K % 64 == 0 GEMMs (the LDS-DMA ring kernel): ragged M, N not a
+    multiple of 8 (element-wise tail stores), and each tile shape."""
+    x, w, b = _mk(m, n, 1024, torch.bfloat16, seed=21, wstd=0.05)
+    y = ext().linear(x.to(dev), w.to(dev), b.to(dev), ACTS[act])
+    close(y, oracle.linear_act(x, w, b, act), what=f"linear {act} {m}x{n}x1024")
+
+
+def test_linear_pipelined_strided_output(dev):
+    """Output rows with a pitch (a column slice of a wider tensor) and K = 3072."""
+    x, w, _ = _mk(2048, 2048, 3072, torch.float16, seed=22, wstd=0.02)
+    out = torch.zeros(2048, 2056, dtype=torch.float16, device=dev)
+    from torchplusplus_amd._native import lib
+    import ctypes
+    xd, wd = x.to(dev), w.to(dev)
+    rc = lib().tpp_linear_act(ctypes.c_void_p(xd.data_ptr()), ctypes.c_void_p(wd.data_ptr()), None,
+                              ctypes.c_void_p(out.data_ptr()), ctypes.c_int64(2048), ctypes.c_int64(2048),
+                              ctypes.c_int64(3072), ctypes.c_int64(3072), ctypes.c_int64(2056),
+                              ctypes.c_int(0), ctypes.c_int(0),
+                              ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    close(out[:, :2048], oracle.linear_act(x, w, None, "none"), what="pitched output")
+    assert torch.count_nonzero(out[:, 2048:]) == 0
+
+
 def test_linear_odd_k_scalar_path(dev):
     x, w, b = _mk(33, 40, 13, torch.float16, seed=2, wstd=0.2)
     y = ext().linear(x.to(dev), w.to(dev), None, ACTS["gelu"])
@@ -97,7 +124,7 @@ def test_gemv_bias_act_and_hgemv_cpu_reference(dev):
     close(y0[0], torch.from_numpy(ref), what="vs hgemvCpu restatement")
 
 
-@pytest.mark.parametrize("rows", [1, 8, 300])
+@pytest.mark.parametrize("rows", [1, 8, 300, 1100])
 def test_swiglu_gemm_and_gemv(dev, rows):
     g = torch.Generator().manual_seed(8)
     I, K = 3072, 1024

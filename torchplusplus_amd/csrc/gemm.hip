@@ -29,6 +29,9 @@ namespace tpp {
 enum GemmEpi { kGPlain = 0, kGBiasAct = 1, kGSwiGLU = 2 };
 
 constexpr int kBM = 128, kBN = 128, kBK = 64;
+// below this many outputs the register-staged kernel's smaller LDS footprint
+// (several blocks per CU) wins over the deeper DMA ring
+constexpr int64_t kDmaMinMN = 256 * 128 * 128;
 
 template <typename T>
 __device__ __forceinline__ f32x16 mfma32(typename VecT<T>::v8 a, typename VecT<T>::v8 b,
@@ -166,6 +169,236 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined variant for K % 64 == 0: operands go HBM/L2 -> LDS directly with
+// global_load_lds_dwordx4 (no VGPR staging, no ds_write), through a 3-stage
+// ring, so two K tiles are in flight while a third is multiplied. Block tile
+// (64*FM) x (64*FN), 4 waves in a 2x2 grid, wave tile (32*FM) x (32*FN).
+// An LDS-DMA instruction writes lane i's 16 bytes at base + 16*i; lane i of
+// a row group therefore fetches the 16-byte chunk kc = (i%8) ^ (row%8), which
+// lands the tile in the same XOR-swizzled layout the fragment reads expect.
+// Waits are explicit (s_waitcnt vmcnt / lgkmcnt + s_barrier): a fenced
+// __syncthreads() would drain every DMA in flight at each K step.
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+constexpr int kDmaStages = 3;
+
+template <int FM, int FN> constexpr int dma_smem_bytes() {
+  return kDmaStages * (64 * FM + 64 * FN) * 128;
+}
+
+template <typename T, int EPI, int ACT, int FM, int FN>
+__global__ __launch_bounds__(256) void gemm_dma_kernel(
+    const T *__restrict__ A, int64_t lda, const T *__restrict__ B, int64_t ldb,
+    T *__restrict__ C, int64_t ldc, const T *__restrict__ bias, int M, int N, int K) {
+  typedef typename VecT<T>::v8 V8;
+  constexpr int BM = 64 * FM, BN = 64 * FN;
+  constexpr int STG = (BM + BN) * 8; // 16-byte slots per stage
+  constexpr int NA = BM / 32, NB = BN / 32; // DMA instructions per wave per stage
+  __shared__ V8 smem[kDmaStages * STG];
+
+  const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w >> 1, wn = w & 1;
+
+  // this lane's source rows for each DMA instruction (clamped to the matrix:
+  // rows past M / N only feed outputs that are never stored)
+  const int lrow = lane >> 3, lkc = (lane & 7) ^ lrow;
+  const T *asrc[NA], *bsrc[NB];
+#pragma unroll
+  for (int j = 0; j < NA; ++j) {
+    const int r = min(m0 + (j * 4 + w) * 8 + lrow, M - 1);
+    asrc[j] = A + (int64_t)r * lda + lkc * 8;
+  }
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int r = min(n0 + (j * 4 + w) * 8 + lrow, N - 1);
+    bsrc[j] = B + (int64_t)r * ldb + lkc * 8;
+  }
+  auto issue = [&](int stage, int kt) {
+    V8 *sa = smem + stage * STG, *sb = sa + BM * 8;
+    const int64_t ko = (int64_t)kt * 64;
+#pragma unroll
+    for (int j = 0; j < NA; ++j)
+      __builtin_amdgcn_global_load_lds((const void *)(asrc[j] + ko),
+                                       (__attribute__((address_space(3))) void *)(sa + (j * 4 + w) * 64),
+                                       16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      __builtin_amdgcn_global_load_lds((const void *)(bsrc[j] + ko),
+                                       (__attribute__((address_space(3))) void *)(sb + (j * 4 + w) * 64),
+                                       16, 0, 0);
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = K / 64;
+  issue(0, 0);
+  if (nk > 1) issue(1, 1);
+  for (int kt = 0; kt < nk; ++kt) {
+    // own DMA of tile kt complete (tile kt+1 may still be in flight), own
+    // reads of tile kt-1 complete; then the barrier publishes both
+    if (kt + 1 < nk)
+      wait_vmcnt<NA + NB>();
+    else
+      wait_vmcnt<0>();
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    if (kt + 2 < nk) issue((kt + 2) % kDmaStages, kt + 2);
+    const V8 *sa = smem + (kt % kDmaStages) * STG, *sb = sa + BM * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int kc = ks * 2 + (lane >> 5);
+      V8 af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = wm * FM * 32 + i * 32 + (lane & 31);
+        af[i] = sa[row * 8 + (kc ^ (row & 7))];
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int col = wn * FN * 32 + j * 32 + (lane & 31);
+        bfr[j] = sb[col * 8 + (kc ^ (col & 7))];
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32<T>(bfr[j], af[i], acc[i][j]);
+    }
+  }
+
+  // Epilogue. The operands are swapped in the MFMA (W rows first), so the
+  // 32x32 accumulator holds lane -> output row m = i*32 + (lane & 31) and
+  // registers 4q..4q+3 -> four consecutive output columns
+  // n = j*32 + q*8 + (lane/32)*4 + {0..3}. Each wave converts its 32FM x 32FN
+  // tile, packs 4 columns per 8-byte LDS write into a padded row-major
+  // staging tile (the ring is free by now), then stores whole rows with
+  // 16-byte global writes.
+  constexpr int OW = (EPI == kGSwiGLU) ? FN * 16 : FN * 32; // output cols per wave
+  constexpr int LDR = OW + 8; // staging row pitch in elements (16-byte aligned rows)
+  static_assert(4 * FM * 32 * LDR * (int)sizeof(T) <= kDmaStages * STG * 16, "staging fits the ring");
+  wait_lgkmcnt0();
+  __builtin_amdgcn_s_barrier(); // every wave is done reading the ring
+  T *stage = reinterpret_cast<T *>(smem) + w * (FM * 32 * LDR);
+  const int half = lane >> 5, ml = lane & 31;
+  const int nw0 = n0 + wn * FN * 32; // first W row (output column before SwiGLU) of the wave
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    if constexpr (EPI == kGSwiGLU) {
+      if (j & 1) continue;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int nl = j * 32 + q * 8 + half * 4; // wave-local W column of register 4q
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (EPI == kGBiasAct) {
+        if (bias) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[e] = nw0 + nl + e < N ? to_f32(bias[nw0 + nl + e]) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        typename VecT<T>::v4 pk;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = acc[i][j][4 * q + e];
+          if constexpr (EPI == kGSwiGLU) {
+            const float gt = to_f32(from_f32<T>(v));
+            const float sl = to_f32(from_f32<T>(act_silu(gt)));
+            v = sl * to_f32(from_f32<T>(acc[i][j + 1][4 * q + e]));
+          } else if constexpr (EPI == kGBiasAct) {
+            v = apply_act<ACT>(to_f32(from_f32<T>(v + bv[e])));
+          }
+          pk[e] = from_f32<T>(v);
+        }
+        const int col = (EPI == kGSwiGLU) ? (j / 2) * 32 + q * 8 + half * 4 : nl;
+        *reinterpret_cast<typename VecT<T>::v4 *>(stage + (i * 32 + ml) * LDR + col) = pk;
+      }
+    }
+  }
+  wait_lgkmcnt0();
+  // rows of the wave tile: OW/8 lanes per row, 16 bytes each; RPI rows per
+  // pass (with OW = 96, lanes 60..63 idle)
+  constexpr int LPR = OW / 8, RPI = 64 / LPR;
+  const int oc0 = (EPI == kGSwiGLU) ? nw0 / 2 : nw0;
+  const int NO = (EPI == kGSwiGLU) ? N / 2 : N;
+  const int rr = lane / LPR, cc = (lane % LPR) * 8;
+  const bool vec_ok = (ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+#pragma unroll
+  for (int r0 = 0; r0 < FM * 32; r0 += RPI) {
+    const int rl = r0 + rr;
+    if (rr >= RPI || rl >= FM * 32) continue;
+    const int row = m0 + wm * FM * 32 + rl;
+    const typename VecT<T>::v8 v =
+        *reinterpret_cast<const typename VecT<T>::v8 *>(stage + rl * LDR + cc);
+    if (row >= M) continue;
+    const int col = oc0 + cc;
+    T *dst = C + (int64_t)row * ldc + col;
+    if (vec_ok && col + 8 <= NO) {
+      *reinterpret_cast<typename VecT<T>::v8 *>(dst) = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (col + e < NO) dst[e] = v[e];
+    }
+  }
+}
+
+// Tile shape for the DMA kernel: minimise rounds-of-tiles x tile work /
+// main-loop efficiency (one block per CU: the ring takes 96-144 KB of LDS).
+// Efficiencies are the measured LDS->MFMA throughput of each wave tile.
+static int pick_dma_tile(int64_t M, int64_t N, bool swiglu, int cus) {
+  struct Cand { int fm, fn; double eff; };
+  const Cand cands[] = {{2, 2, 0.86}, {2, 3, 0.88}, {2, 4, 0.91}};
+  int best = -1;
+  double best_t = 0.0;
+  for (int c = 0; c < 3; ++c) {
+    if (swiglu && (cands[c].fn & 1)) continue;
+    const int64_t bm = 64 * cands[c].fm, bn = 64 * cands[c].fn;
+    const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const int64_t rounds = (tiles + cus - 1) / cus;
+    const double t = (double)rounds * (double)(bm * bn) / cands[c].eff;
+    if (best < 0 || t < best_t) best = c, best_t = t;
+  }
+  return best;
+}
+
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <typename T, int EPI, int ACT, int FM, int FN>
+static void launch_dma(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
+                       int64_t ldc, const void *bias, int64_t M, int64_t N, int64_t K,
+                       hipStream_t st) {
+  const int64_t nb = ((M + 64 * FM - 1) / (64 * FM)) * ((N + 64 * FN - 1) / (64 * FN));
+  gemm_dma_kernel<T, EPI, ACT, FM, FN><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+      (const T *)A, lda, (const T *)B, ldb, (T *)C, ldc, (const T *)bias, (int)M, (int)N, (int)K);
+}
+
 // Fallback for K % 8 != 0 or unaligned operands: one thread per output.
 template <typename T, int EPI, int ACT>
 __global__ __launch_bounds__(256) void gemm_scalar_kernel(
@@ -202,7 +435,15 @@ static int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, v
   if (M == 0) return TPP_OK;
   const bool vec = (K % 8 == 0) && (lda % 8 == 0) && (ldb % 8 == 0) && aligned16(A) &&
                    aligned16(B);
-  if (vec) {
+  if (vec && K % 64 == 0 && M * N >= (int64_t)kDmaMinMN) {
+    if ((M + 127) / 128 * ((N + 127) / 128) > 0x7fffffffLL)
+      return set_error(TPP_E_UNSUPPORTED, "%s: too many tiles", name);
+    switch (pick_dma_tile(M, N, EPI == kGSwiGLU, device_cus())) {
+    case 0: launch_dma<T, EPI, ACT, 2, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 1: launch_dma<T, EPI, ACT, 2, 3>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    default: launch_dma<T, EPI, ACT, 2, 4>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    }
+  } else if (vec) {
     const int64_t nb = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
     if (nb > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: too many tiles", name);
     gemm_kernel<T, EPI, ACT><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
