@@ -103,6 +103,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   constexpr int NS = kGemvWaveK / 32; // MFMA steps per wave batch
   __shared__ f32x4 red[EPI == kEpiSwiGLU ? 2 : 1][MAXW][64];
   __shared__ float s_inv[16];
+  __shared__ float s_part[MAXW][16];
   const int lane = lane_id(), w = wave_id(), nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t N = a.N, K = a.K;
@@ -112,52 +113,6 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   const T *xr = X + (xok ? r : 0) * a.ldx;
   const int64_t k_begin = (int64_t)w * a.kslice;
   const int64_t k_end = k_begin + a.kslice < K ? k_begin + a.kslice : K;
-
-  if constexpr (NORM) {
-    // inv_rms of the <= 16 input rows (wave w: rows w, w + nw, ..)
-    for (int row = w; row < a.NB; row += nw) {
-      const T *xp = X + row * a.ldx;
-      float ss = 0.f;
-      for (int64_t c = (int64_t)lane * 8; c < K; c += 64 * 8) {
-        float v[8];
-        load8(xp + c, v);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
-      }
-      ss = wave_sum(ss);
-      if (lane == 0) s_inv[row] = rsqrtf(ss / (float)K + a.eps);
-    }
-    __syncthreads();
-  }
-  // this wave's slice of the (normalised) input, reused by every tile
-  // kept resident when the wave's K slice is one load batch (K <= 4096 for
-  // plain GEMVs, 2048 for SwiGLU); longer slices reload x per batch
-  const bool x_res = k_end - k_begin <= kGemvWaveK;
-  V8 xa[NS];
-  auto load_x = [&](int64_t k, V8 (&dst)[NS]) {
-#pragma unroll
-    for (int u = 0; u < NS; ++u) {
-      const int64_t c = k + u * 32 + g * 8; // K % 8 == 0: a chunk is all in or all out
-      const bool ok = c < k_end && xok;
-      dst[u] = ld16(xr + c, ok);
-      if constexpr (NORM) {
-        if (ok) {
-          float xv[8], nv[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) xv[i] = to_f32(dst[u][i]);
-          load8((const T *)a.norm_w + c, nv);
-          const float inv = s_inv[r];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) dst[u][i] = from_f32<T>((xv[i] * inv) * nv[i]);
-        }
-      }
-    }
-  };
-  if (x_res) load_x(k_begin, xa);
-
-  // per-block running argmax over all tiles (wave 0, lanes r == 0 hold it)
-  float am_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  int am_i[4] = {0x7fffffff, 0x7fffffff, 0x7fffffff, 0x7fffffff};
 
   auto rows_of = [&](int64_t tile, int64_t &row0, int64_t &row1) {
     if constexpr (EPI == kEpiSwiGLU) {
@@ -194,6 +149,95 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       }
     }
   };
+  // one K batch per wave: x stays resident. With the fused RMSNorm the
+  // weights of the block's first tile are requested before the input
+  // prologue (row statistics, barrier, x loads), so the two latency chains
+  // overlap; without it x is requested first.
+  const bool x_res = k_end - k_begin <= kGemvWaveK;
+  V8 pa0[NS], pa1[NS], pb0[NS], pb1[NS];
+  float ra[4] = {0.f, 0.f, 0.f, 0.f}, rb[4] = {0.f, 0.f, 0.f, 0.f};
+  if (NORM && x_res && blockIdx.x < tiles) load_w(blockIdx.x, k_begin, pa0, pa1, ra);
+
+  // this wave's slice of the (normalised) input, reused by every tile
+  // kept resident when the wave's K slice is one load batch (K <= 4096 for
+  // plain GEMVs, 2048 for SwiGLU); longer slices reload x per batch
+  V8 xa[NS];
+  auto load_x = [&](int64_t k, V8 (&dst)[NS]) {
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int64_t c = k + u * 32 + g * 8; // K % 8 == 0: a chunk is all in or all out
+      const bool ok = c < k_end && xok;
+      dst[u] = ld16(xr + c, ok);
+      if constexpr (NORM) {
+        if (ok) {
+          float xv[8], nv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) xv[i] = to_f32(dst[u][i]);
+          load8((const T *)a.norm_w + c, nv);
+          const float inv = s_inv[r];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dst[u][i] = from_f32<T>((xv[i] * inv) * nv[i]);
+        }
+      }
+    }
+  };
+  if constexpr (NORM) {
+    if (x_res) {
+      // the wave's raw slice doubles as its share of the row statistics:
+      // partial sums of squares over the K slices meet in LDS, so the input
+      // is read once and there is one barrier before the normalisation
+      V8 nwv[NS];
+#pragma unroll
+      for (int u = 0; u < NS; ++u) {
+        const int64_t c = k_begin + u * 32 + g * 8;
+        xa[u] = ld16(xr + c, c < k_end && xok);
+        nwv[u] = ld16((const T *)a.norm_w + c, c < k_end);
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int u = 0; u < NS; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float v = to_f32(xa[u][i]);
+          ss += v * v;
+        }
+      ss += __shfl_xor(ss, 16, kWave); // lanes r, r+16, r+32, r+48: row r
+      ss += __shfl_xor(ss, 32, kWave);
+      if (g == 0) s_part[w][r] = ss;
+      __syncthreads();
+      float tot = 0.f;
+      for (int i = 0; i < nw; ++i) tot += s_part[i][r];
+      const float inv = rsqrtf(tot / (float)K + a.eps);
+#pragma unroll
+      for (int u = 0; u < NS; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          xa[u][i] = from_f32<T>((to_f32(xa[u][i]) * inv) * to_f32(nwv[u][i]));
+    } else {
+      // inv_rms of the <= 16 input rows (wave w: rows w, w + nw, ..)
+      for (int row = w; row < a.NB; row += nw) {
+        const T *xp = X + row * a.ldx;
+        float ss = 0.f;
+        for (int64_t c = (int64_t)lane * 8; c < K; c += 64 * 8) {
+          float v[8];
+          load8(xp + c, v);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) s_inv[row] = rsqrtf(ss / (float)K + a.eps);
+      }
+      __syncthreads();
+    }
+  } else if (x_res) {
+    load_x(k_begin, xa);
+    if (blockIdx.x < tiles) load_w(blockIdx.x, k_begin, pa0, pa1, ra);
+  }
+
+  // per-block running argmax over all tiles (wave 0, lanes r == 0 hold it)
+  float am_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  int am_i[4] = {0x7fffffff, 0x7fffffff, 0x7fffffff, 0x7fffffff};
+
   // block-wide K reduction of a tile's accumulators and its epilogue
   auto finish = [&](int64_t tile, f32x4 acc0, f32x4 acc1, const float (&res_in)[4]) {
     int64_t row0, row1;
@@ -261,11 +305,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   if (x_res) {
     // one K batch per wave: keep two tiles in flight (W of tile t + stride is
     // requested before tile t is reduced and written)
-    V8 pa0[NS], pa1[NS], pb0[NS], pb1[NS];
-    float ra[4] = {0.f, 0.f, 0.f, 0.f}, rb[4] = {0.f, 0.f, 0.f, 0.f};
-    int64_t t = blockIdx.x;
-    if (t < tiles) load_w(t, k_begin, pa0, pa1, ra);
-    for (; t < tiles; t += 2 * stride) {
+    for (int64_t t = blockIdx.x; t < tiles; t += 2 * stride) {
       const int64_t t2 = t + stride;
       if (t2 < tiles) load_w(t2, k_begin, pb0, pb1, rb);
       f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
