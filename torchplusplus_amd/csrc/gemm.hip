@@ -171,9 +171,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 
 // ---------------------------------------------------------------------------
 // Pipelined variant for K % 64 == 0: operands go HBM/L2 -> LDS directly with
-// global_load_lds_dwordx4 (no VGPR staging, no ds_write), through a 3-stage
-// ring, so two K tiles are in flight while a third is multiplied. Block tile
-// (64*FM) x (64*FN), 4 waves in a 2x2 grid, wave tile (32*FM) x (32*FN).
+// global_load_lds_dwordx4 (no VGPR staging, no ds_write), through an
+// NST-stage ring (NST-1 K tiles in flight while one is multiplied). Block
+// tile (64*FM) x (64*FN), 4 waves in a 2x2 grid, wave tile (32*FM) x (32*FN).
+// Why big tiles: the CU's L1 delivers ~64 B/clk while its four matrix cores
+// consume 4096 bf16 flop/clk, so a BM x BN tile needs (BM+BN)/(BM*BN) <=
+// 1/64 byte per flop; 128x128 sits exactly at that limit, 256x256 at half.
+// Measured on MI355X: 256x256 (one block per CU) runs ~36-40% of MFMA peak
+// on the prefill shapes vs ~31% for 128x128; with fewer tiles than CUs the
+// 128-row tiles (two blocks per CU with a 2-stage ring) win.
 // An LDS-DMA instruction writes lane i's 16 bytes at base + 16*i; lane i of
 // a row group therefore fetches the 16-byte chunk kc = (i%8) ^ (row%8), which
 // lands the tile in the same XOR-swizzled layout the fragment reads expect.
@@ -185,13 +191,7 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-constexpr int kDmaStages = 3;
-
-template <int FM, int FN> constexpr int dma_smem_bytes() {
-  return kDmaStages * (64 * FM + 64 * FN) * 128;
-}
-
-template <typename T, int EPI, int ACT, int FM, int FN>
+template <typename T, int EPI, int ACT, int FM, int FN, int NST>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(
     const T *__restrict__ A, int64_t lda, const T *__restrict__ B, int64_t ldb,
     T *__restrict__ C, int64_t ldc, const T *__restrict__ bias, int M, int N, int K) {
@@ -199,7 +199,10 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(
   constexpr int BM = 64 * FM, BN = 64 * FN;
   constexpr int STG = (BM + BN) * 8; // 16-byte slots per stage
   constexpr int NA = BM / 32, NB = BN / 32; // DMA instructions per wave per stage
-  __shared__ V8 smem[kDmaStages * STG];
+  // the epilogue's staging tile reuses the ring
+  constexpr int OWS = (EPI == kGSwiGLU) ? FN * 16 : FN * 32;
+  constexpr int RING = NST * STG, OUTS = 4 * FM * 32 * (OWS + 8) * (int)sizeof(T) / 16;
+  __shared__ V8 smem[RING > OUTS ? RING : OUTS];
 
   const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
   int tm, tn;
@@ -208,31 +211,22 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w >> 1, wn = w & 1;
 
-  // this lane's source rows for each DMA instruction (clamped to the matrix:
-  // rows past M / N only feed outputs that are never stored)
+  // DMA instruction j of wave w covers tile rows (4j + w)*8 .. +7; lane i
+  // fetches row +i/8, chunk (i%8)^(row%8). Source rows are clamped to the
+  // matrix: rows past M / N only feed outputs that are never stored.
   const int lrow = lane >> 3, lkc = (lane & 7) ^ lrow;
-  const T *asrc[NA], *bsrc[NB];
-#pragma unroll
-  for (int j = 0; j < NA; ++j) {
-    const int r = min(m0 + (j * 4 + w) * 8 + lrow, M - 1);
-    asrc[j] = A + (int64_t)r * lda + lkc * 8;
-  }
-#pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const int r = min(n0 + (j * 4 + w) * 8 + lrow, N - 1);
-    bsrc[j] = B + (int64_t)r * ldb + lkc * 8;
-  }
+  const int arow = m0 + w * 8 + lrow, brow = n0 + w * 8 + lrow;
   auto issue = [&](int stage, int kt) {
     V8 *sa = smem + stage * STG, *sb = sa + BM * 8;
-    const int64_t ko = (int64_t)kt * 64;
+    const int64_t ko = (int64_t)kt * 64 + lkc * 8;
 #pragma unroll
     for (int j = 0; j < NA; ++j)
-      __builtin_amdgcn_global_load_lds((const void *)(asrc[j] + ko),
+      __builtin_amdgcn_global_load_lds((const void *)(A + (int64_t)min(arow + 32 * j, M - 1) * lda + ko),
                                        (__attribute__((address_space(3))) void *)(sa + (j * 4 + w) * 64),
                                        16, 0, 0);
 #pragma unroll
     for (int j = 0; j < NB; ++j)
-      __builtin_amdgcn_global_load_lds((const void *)(bsrc[j] + ko),
+      __builtin_amdgcn_global_load_lds((const void *)(B + (int64_t)min(brow + 32 * j, N - 1) * ldb + ko),
                                        (__attribute__((address_space(3))) void *)(sb + (j * 4 + w) * 64),
                                        16, 0, 0);
   };
@@ -246,19 +240,24 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int nk = K / 64;
-  issue(0, 0);
-  if (nk > 1) issue(1, 1);
+#pragma unroll
+  for (int p = 0; p < NST - 1; ++p)
+    if (p < nk) issue(p, p);
   for (int kt = 0; kt < nk; ++kt) {
-    // own DMA of tile kt complete (tile kt+1 may still be in flight), own
+    // own DMA of tile kt complete (later tiles may still be in flight), own
     // reads of tile kt-1 complete; then the barrier publishes both
-    if (kt + 1 < nk)
-      wait_vmcnt<NA + NB>();
-    else
+    if constexpr (NST == 2) {
       wait_vmcnt<0>();
+    } else {
+      if (kt + 1 < nk)
+        wait_vmcnt<(NST - 2) * (NA + NB)>();
+      else
+        wait_vmcnt<0>();
+    }
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
-    if (kt + 2 < nk) issue((kt + 2) % kDmaStages, kt + 2);
-    const V8 *sa = smem + (kt % kDmaStages) * STG, *sb = sa + BM * 8;
+    if (kt + NST - 1 < nk) issue((kt + NST - 1) % NST, kt + NST - 1);
+    const V8 *sa = smem + (kt % NST) * STG, *sb = sa + BM * 8;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int kc = ks * 2 + (lane >> 5);
@@ -289,12 +288,12 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(
   // 16-byte global writes.
   constexpr int OW = (EPI == kGSwiGLU) ? FN * 16 : FN * 32; // output cols per wave
   constexpr int LDR = OW + 8; // staging row pitch in elements (16-byte aligned rows)
-  static_assert(4 * FM * 32 * LDR * (int)sizeof(T) <= kDmaStages * STG * 16, "staging fits the ring");
   wait_lgkmcnt0();
   __builtin_amdgcn_s_barrier(); // every wave is done reading the ring
   T *stage = reinterpret_cast<T *>(smem) + w * (FM * 32 * LDR);
   const int half = lane >> 5, ml = lane & 31;
   const int nw0 = n0 + wn * FN * 32; // first W row (output column before SwiGLU) of the wave
+  const bool bias_vec = (reinterpret_cast<uintptr_t>(bias) & 7) == 0;
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     if constexpr (EPI == kGSwiGLU) {
@@ -306,8 +305,15 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(
       float bv[4] = {0.f, 0.f, 0.f, 0.f};
       if constexpr (EPI == kGBiasAct) {
         if (bias) {
+          const int c0 = nw0 + nl;
+          if (bias_vec && c0 + 4 <= N) { // one 8-byte load for the 4 columns
+            const typename VecT<T>::v4 b4 = *reinterpret_cast<const typename VecT<T>::v4 *>(bias + c0);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) bv[e] = nw0 + nl + e < N ? to_f32(bias[nw0 + nl + e]) : 0.f;
+            for (int e = 0; e < 4; ++e) bv[e] = to_f32(b4[e]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[e] = c0 + e < N ? to_f32(bias[c0 + e]) : 0.f;
+          }
         }
       }
 #pragma unroll
@@ -358,20 +364,21 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(
   }
 }
 
-// Tile shape for the DMA kernel: minimise rounds-of-tiles x tile work /
-// main-loop efficiency (one block per CU: the ring takes 96-144 KB of LDS).
-// Efficiencies are the measured LDS->MFMA throughput of each wave tile.
+// Tile shape for the DMA kernel: minimise (tiles per CU, rounded up) x tile
+// area / relative efficiency. Candidates are 2-stage rings; the 128-row ones
+// fit two blocks per CU (<= 80 KB of LDS). SwiGLU needs whole [gate|up]
+// 64-column pairs per wave (FN even).
 static int pick_dma_tile(int64_t M, int64_t N, bool swiglu, int cus) {
   struct Cand { int fm, fn; double eff; };
-  const Cand cands[] = {{2, 2, 0.86}, {2, 3, 0.88}, {2, 4, 0.91}};
+  const Cand cands[] = {{2, 2, 0.95}, {2, 3, 1.0}, {2, 4, 1.0}, {4, 4, 1.15}};
   int best = -1;
   double best_t = 0.0;
-  for (int c = 0; c < 3; ++c) {
+  for (int c = 0; c < 4; ++c) {
     if (swiglu && (cands[c].fn & 1)) continue;
     const int64_t bm = 64 * cands[c].fm, bn = 64 * cands[c].fn;
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    const int64_t rounds = (tiles + cus - 1) / cus;
-    const double t = (double)rounds * (double)(bm * bn) / cands[c].eff;
+    const int64_t per_cu = (tiles + cus - 1) / cus;
+    const double t = (double)per_cu * (double)(bm * bn) / cands[c].eff;
     if (best < 0 || t < best_t) best = c, best_t = t;
   }
   return best;
@@ -395,7 +402,7 @@ static void launch_dma(const void *A, int64_t lda, const void *B, int64_t ldb, v
                        int64_t ldc, const void *bias, int64_t M, int64_t N, int64_t K,
                        hipStream_t st) {
   const int64_t nb = ((M + 64 * FM - 1) / (64 * FM)) * ((N + 64 * FN - 1) / (64 * FN));
-  gemm_dma_kernel<T, EPI, ACT, FM, FN><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+  gemm_dma_kernel<T, EPI, ACT, FM, FN, 2><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
       (const T *)A, lda, (const T *)B, ldb, (T *)C, ldc, (const T *)bias, (int)M, (int)N, (int)K);
 }
 
@@ -441,7 +448,8 @@ static int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, v
     switch (pick_dma_tile(M, N, EPI == kGSwiGLU, device_cus())) {
     case 0: launch_dma<T, EPI, ACT, 2, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
     case 1: launch_dma<T, EPI, ACT, 2, 3>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    default: launch_dma<T, EPI, ACT, 2, 4>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 2: launch_dma<T, EPI, ACT, 2, 4>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    default: launch_dma<T, EPI, ACT, 4, 4>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
     }
   } else if (vec) {
     const int64_t nb = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);

@@ -157,13 +157,18 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
 
 // ---- activations (fp32), csrc/activation/activation.cuh:26-67 -------------
+// Both use the hardware exp2-based __expf and the v_rcp_f32 reciprocal
+// (~1 ulp) instead of IEEE division / libm tanhf: the epilogue of a GEMM tile
+// evaluates ~100 of these per lane with nothing to overlap them.
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+// 0.5 x (1 + tanh(u)) == x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
 __device__ __forceinline__ float act_gelu_tanh(float x) {
   const float kAlpha = 0.7978845608028654f; // sqrt(2/pi)
   const float kBeta = 0.044715f;
-  float t = tanhf(kAlpha * (x + kBeta * x * x * x));
-  return 0.5f * x * (1.0f + t);
+  const float u = kAlpha * (x + kBeta * x * x * x);
+  return x * fast_rcp(1.0f + __expf(-2.0f * u));
 }
-__device__ __forceinline__ float act_silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float act_silu(float x) { return x * fast_rcp(1.0f + __expf(-x)); }
 __device__ __forceinline__ float act_relu(float x) { return fmaxf(0.0f, x); }
 
 template <int ACT> __device__ __forceinline__ float apply_act(float x) {
