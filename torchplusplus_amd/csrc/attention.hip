@@ -62,6 +62,13 @@ struct DecodeFuse {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kKvTile = 64;
+// 32-query groups per prefill wave (each K / V^T fragment read from LDS feeds
+// every group's products). Two groups need more than the 512 VGPRs of a wave
+// at D = 128 and spill, so one group is used.
+constexpr int kPrefillQG = 1;
+// waves per prefill block: 8 = two per SIMD, so one wave's softmax (VALU)
+// overlaps the other's MFMAs
+constexpr int kPrefillWaves = 8;
 
 template <typename T>
 __device__ __forceinline__ f32x16 mfma32x32(typename VecT<T>::v8 a, typename VecT<T>::v8 b,
@@ -80,8 +87,8 @@ template <typename T, int D> struct PrefillSmem {
   uint64_t vt[2][D * 16];    // [d][slot ^ vt_swz(d)], slot = 4 keys
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs p, int hpb) {
+template <typename T, int D, int QG, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int hpb) {
   typedef typename VecT<T>::v8 V8;
   constexpr int CPR = D / 8; // 16-byte chunks per row
   constexpr int NT = D / 32; // 32-row MFMA tiles along D
@@ -90,8 +97,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs p, int hpb) 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int h = lane >> 5, ql = lane & 31;
   const int G = p.Hq / p.Hkv;
-  const int wph = 4 / hpb;   // waves per head
-  const int qt_len = wph * 32;
+  const int wph = NW / hpb;  // waves per head
+  const int qt_len = wph * 32 * QG;
   const int nqt = (p.Sq + qt_len - 1) / qt_len;
   const int nhg = p.Hq / hpb;
   const int bid = blockIdx.x;
@@ -102,7 +109,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs p, int hpb) 
   const int hk = (hg * hpb) / G;
   const int q0 = qt * qt_len;
   const int q_last = (q0 + qt_len < p.Sq ? q0 + qt_len : p.Sq) - 1;
-  const int qi = q0 + (w % wph) * 32 + ql;
+  const int qw = q0 + (w % wph) * 32 * QG; // first query of this wave
   const int off = p.Sk - p.Sq;
 
   // key band of the whole block
@@ -126,25 +133,39 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs p, int hpb) 
 #pragma unroll
   for (int i = 0; i < 8; ++i) zero[i] = (T)0.0f;
 
-  V8 qf[D / 16];
+  // QG groups of 32 queries per wave share every K / V fragment read from LDS
+  V8 qf[QG][D / 16];
 #pragma unroll
-  for (int ks = 0; ks < D / 16; ++ks)
-    qf[ks] = qi < p.Sq ? *reinterpret_cast<const V8 *>(qp + (int64_t)qi * p.q_ss + ks * 16 + h * 8)
-                       : zero;
+  for (int g = 0; g < QG; ++g) {
+    const int qi = qw + g * 32 + ql;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+      qf[g][ks] = qi < p.Sq
+                      ? *reinterpret_cast<const V8 *>(qp + (int64_t)qi * p.q_ss + ks * 16 + h * 8)
+                      : zero;
+  }
 
-  // staging registers for the next tile
-  constexpr int KCH = kKvTile * CPR / 256; // K chunks per thread (4 for D=128)
-  V8 rk[KCH];
+  // K tiles go HBM/L2 -> LDS by LDS-DMA (no staging registers): instruction
+  // i of wave w fills 64 slots = 64/CPR keys; lane l fetches the chunk that
+  // lands in its slot, chunk (l % CPR) ^ (key % CPR). Keys past Sk are
+  // clamped to Sk-1 (finite data; those scores are masked on the edge tile).
+  // V^T tiles are transposed through VGPRs.
+  constexpr int KPI = 64 / CPR;                 // keys per DMA instruction
+  constexpr int KDMA = kKvTile / KPI / NW;      // DMA instructions per wave per tile
+  const int dkey = lane / CPR, dslot = lane % CPR;
   V8 rv[4];
   const bool vthread = tid < 16 * CPR;
   const int vkg = tid / CPR, vch = tid % CPR;
-  auto gload = [&](int t) {
+  auto gload = [&](int t, int buf) {
     const int kb = t * kKvTile;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + 256 * i, key = c / CPR, ch = c % CPR;
-      const int kk = kb + key;
-      rk[i] = kk < p.Sk ? *reinterpret_cast<const V8 *>(kp + (int64_t)kk * p.k_ss + ch * 8) : zero;
+    for (int i = 0; i < KDMA; ++i) {
+      const int key0 = (i * NW + w) * KPI; // first key of the instruction
+      const int key = key0 + dkey, ch = dslot ^ (key & (CPR - 1));
+      const int kk = min(kb + key, p.Sk - 1);
+      __builtin_amdgcn_global_load_lds(
+          (const void *)(kp + (int64_t)kk * p.k_ss + ch * 8),
+          (__attribute__((address_space(3))) void *)&sm.k[buf][key0 * CPR], 16, 0, 0);
     }
     if (vthread) {
 #pragma unroll
@@ -156,11 +177,6 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs p, int hpb) 
     }
   };
   auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + 256 * i, key = c / CPR, ch = c % CPR;
-      sm.k[buf][key * CPR + (ch ^ (key & (CPR - 1)))] = rk[i];
-    }
     if (vthread) {
       // Whole-vector bit casts: hipcc (clang 22) miscompiles a bit cast of a
       // single __bf16 ext-vector element into a read of element 0.
@@ -178,84 +194,103 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs p, int hpb) 
     }
   };
 
-  f32x16 o[NT];
+  f32x16 o[QG][NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int g = 0; g < QG; ++g)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[g][t][r] = 0.f;
+  float m_run[QG], l_run[QG];
+#pragma unroll
+  for (int g = 0; g < QG; ++g) m_run[g] = -INFINITY, l_run[g] = 0.f;
 
   if (t_begin < t_end) {
-    gload(t_begin);
+    gload(t_begin, 0);
     sstore(0);
   }
-  __syncthreads();
+  __syncthreads(); // (its fence also drains the K DMA)
   for (int t = t_begin; t < t_end; ++t) {
     const int buf = (t - t_begin) & 1;
-    if (t + 1 < t_end) gload(t + 1);
+    if (t + 1 < t_end) gload(t + 1, buf ^ 1);
     const int kb = t * kKvTile;
 
-    f32x16 s[2];
+    f32x16 s[QG][2];
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int g = 0; g < QG; ++g)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[st][r] = 0.f;
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[g][st][r] = 0.f;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         const int key = st * 32 + ql, ch = ks * 2 + h;
         const V8 a = sm.k[buf][key * CPR + (ch ^ (key & (CPR - 1)))];
-        s[st] = mfma32x32<T>(a, qf[ks], s[st]);
+#pragma unroll
+        for (int g = 0; g < QG; ++g) s[g][st] = mfma32x32<T>(a, qf[g][ks], s[g][st]);
       }
     }
-    // scores -> log2 domain, masking on band edges only
+    // Online softmax on raw scores: the running max m is kept unscaled and
+    // exp2(scale*log2e*(s - m)) is one FMA + v_exp_f32 per score (scale > 0
+    // preserves the max). Masking only on band edges.
     const bool edge = (p.right >= 0 && kb + kKvTile - 1 > q0 + off + p.right) ||
                       (p.left >= 0 && kb < q_last + off - p.left) || (kb + kKvTile > p.Sk);
-    float mt = -INFINITY;
+    const float c2 = p.scale_log2;
+    V8 pb[QG][4];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
+    for (int g = 0; g < QG; ++g) {
+      const int qi = qw + g * 32 + ql;
+      float mt = -INFINITY;
+      if (edge) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[st][r] * p.scale_log2;
-        if (edge) {
-          const int j = kb + st * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-          const int rel = j - (qi + off);
-          bool keep = j < p.Sk;
-          if (p.right >= 0) keep = keep && rel <= p.right;
-          if (p.left >= 0) keep = keep && rel >= -p.left;
-          x = keep ? x : -INFINITY;
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int j = kb + st * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+            const int rel = j - (qi + off);
+            bool keep = j < p.Sk;
+            if (p.right >= 0) keep = keep && rel <= p.right;
+            if (p.left >= 0) keep = keep && rel >= -p.left;
+            s[g][st][r] = keep ? s[g][st][r] : -INFINITY;
+          }
+      }
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[g][st][r]);
+      mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+      const float m_new = fmaxf(m_run[g], mt);
+      const float mc = m_new == -INFINITY ? 0.f : m_new * c2;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[g] * c2 - mc);
+      float psum = 0.f;
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(s[g][st][r], c2, -mc));
+          s[g][st][r] = e;
+          psum += e;
         }
-        s[st][r] = x;
-        mt = fmaxf(mt, x);
+      l_run[g] = l_run[g] * alpha + psum;
+      m_run[g] = m_new;
+      // the running max rarely moves after the first tiles: skip the O
+      // rescale (a multiply by exactly 1) unless some lane's max changed
+      if (__any(alpha != 1.f)) {
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[g][tt][r] *= alpha;
       }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pb[g][c][j] = from_f32<T>(s[g][c >> 1][(c & 1) * 8 + j]);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float m_new = fmaxf(m_run, mt);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    float psum = 0.f;
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = exp2f(s[st][r] - m_use);
-        s[st][r] = e;
-        psum += e;
-      }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int tt = 0; tt < NT; ++tt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[tt][r] *= alpha;
 
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int st = c >> 1, c2 = c & 1;
-      V8 pb;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pb[j] = from_f32<T>(s[st][c2 * 8 + j]);
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt) {
         const int d = tt * 32 + ql;
@@ -264,27 +299,32 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs p, int hpb) 
         const uint64_t u1 = sm.vt[buf][d * 16 + ((4 * c + 2 + h) ^ sw)];
         u32x4 raw = {(uint32_t)u0, (uint32_t)(u0 >> 32), (uint32_t)u1, (uint32_t)(u1 >> 32)};
         const V8 a = __builtin_bit_cast(V8, raw);
-        o[tt] = mfma32x32<T>(a, pb, o[tt]);
+#pragma unroll
+        for (int g = 0; g < QG; ++g) o[g][tt] = mfma32x32<T>(a, pb[g][c], o[g][tt]);
       }
     }
     if (t + 1 < t_end) sstore(buf ^ 1);
     __syncthreads();
   }
 
-  const float l = l_run + __shfl_xor(l_run, 32, kWave);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  if (qi >= p.Sq) return;
-  T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)qi * p.o_ss + (int64_t)hq * p.o_sh;
   typedef typename VecT<T>::v4 V4;
 #pragma unroll
-  for (int tt = 0; tt < NT; ++tt)
+  for (int g = 0; g < QG; ++g) {
+    const float l = l_run[g] + __shfl_xor(l_run[g], 32, kWave);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int qi = qw + g * 32 + ql;
+    if (qi >= p.Sq) continue;
+    T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)qi * p.o_ss + (int64_t)hq * p.o_sh;
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      V4 pk;
+    for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pk[i] = from_f32<T>(o[tt][rg * 4 + i] * inv);
-      *reinterpret_cast<V4 *>(op + tt * 32 + rg * 8 + h * 4) = pk;
-    }
+      for (int rg = 0; rg < 4; ++rg) {
+        V4 pk;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pk[i] = from_f32<T>(o[g][tt][rg * 4 + i] * inv);
+        *reinterpret_cast<V4 *>(op + tt * 32 + rg * 8 + h * 4) = pk;
+      }
+  }
 }
 
 // Generic prefill (any D <= 256, any alignment): one wave per (b, query,
@@ -664,14 +704,16 @@ static int launch_prefill(const AttnArgs &a, int64_t D, hipStream_t st, const ch
   const int G = a.Hq / a.Hkv;
   if ((D == 64 || D == 128) && strides16(a)) {
     const int hpb = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
-    const int qt_len = (4 / hpb) * 32;
+    constexpr int QG = kPrefillQG;
+    constexpr int NW = kPrefillWaves;
+    const int qt_len = (NW / hpb) * 32 * QG;
     const int64_t blocks =
         (int64_t)a.B * (a.Hq / hpb) * ((a.Sq + qt_len - 1) / qt_len);
     if (blocks > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: too large", name);
     if (D == 128)
-      attn_prefill_kernel<T, 128><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a, hpb);
+      attn_prefill_kernel<T, 128, QG, NW><<<dim3((unsigned)blocks), dim3(64 * NW), 0, st>>>(a, hpb);
     else
-      attn_prefill_kernel<T, 64><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a, hpb);
+      attn_prefill_kernel<T, 64, QG, NW><<<dim3((unsigned)blocks), dim3(64 * NW), 0, st>>>(a, hpb);
   } else {
     const int64_t blocks = (int64_t)a.B * a.Sq * a.Hq;
     if (blocks > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: too large", name);
