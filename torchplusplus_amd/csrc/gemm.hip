@@ -173,13 +173,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 // Pipelined variant for K % 64 == 0: operands go HBM/L2 -> LDS directly with
 // global_load_lds_dwordx4 (no VGPR staging, no ds_write), through an
 // NST-stage ring (NST-1 K tiles in flight while one is multiplied). Block
-// tile (64*FM) x (64*FN), 4 waves in a 2x2 grid, wave tile (32*FM) x (32*FN).
+// tile (32*WM*FM) x (32*WN*FN), WM x WN waves, wave tile (32*FM) x (32*FN).
 // Why big tiles: the CU's L1 delivers ~64 B/clk while its four matrix cores
 // consume 4096 bf16 flop/clk, so a BM x BN tile needs (BM+BN)/(BM*BN) <=
 // 1/64 byte per flop; 128x128 sits exactly at that limit, 256x256 at half.
-// Measured on MI355X: 256x256 (one block per CU) runs ~36-40% of MFMA peak
-// on the prefill shapes vs ~31% for 128x128; with fewer tiles than CUs the
-// 128-row tiles (two blocks per CU with a 2-stage ring) win.
+// Measured on MI355X: 256x256 with 8 waves (4x2 of 64x128, two per SIMD)
+// runs ~37-43% of MFMA peak on the prefill shapes vs ~31% for 128x128; with
+// fewer tiles than CUs the 128-row tiles (two blocks per CU with a 2-stage
+// ring) win.
 // An LDS-DMA instruction writes lane i's 16 bytes at base + 16*i; lane i of
 // a row group therefore fetches the 16-byte chunk kc = (i%8) ^ (row%8), which
 // lands the tile in the same XOR-swizzled layout the fragment reads expect.
@@ -191,17 +192,17 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-template <typename T, int EPI, int ACT, int FM, int FN, int NST>
-__global__ __launch_bounds__(256) void gemm_dma_kernel(
+template <typename T, int EPI, int ACT, int FM, int FN, int NST, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
     const T *__restrict__ A, int64_t lda, const T *__restrict__ B, int64_t ldb,
     T *__restrict__ C, int64_t ldc, const T *__restrict__ bias, int M, int N, int K) {
   typedef typename VecT<T>::v8 V8;
-  constexpr int BM = 64 * FM, BN = 64 * FN;
+  constexpr int BM = 32 * WM * FM, BN = 32 * WN * FN, NWV = WM * WN;
   constexpr int STG = (BM + BN) * 8; // 16-byte slots per stage
-  constexpr int NA = BM / 32, NB = BN / 32; // DMA instructions per wave per stage
+  constexpr int NA = BM / 8 / NWV, NB = BN / 8 / NWV; // DMA instructions per wave per stage
   // the epilogue's staging tile reuses the ring
   constexpr int OWS = (EPI == kGSwiGLU) ? FN * 16 : FN * 32;
-  constexpr int RING = NST * STG, OUTS = 4 * FM * 32 * (OWS + 8) * (int)sizeof(T) / 16;
+  constexpr int RING = NST * STG, OUTS = NWV * FM * 32 * (OWS + 8) * (int)sizeof(T) / 16;
   __shared__ V8 smem[RING > OUTS ? RING : OUTS];
 
   const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
@@ -209,9 +210,9 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(
   tile_coords(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / WN, wn = w % WN;
 
-  // DMA instruction j of wave w covers tile rows (4j + w)*8 .. +7; lane i
+  // DMA instruction j of wave w covers tile rows (NWV*j + w)*8 .. +7; lane i
   // fetches row +i/8, chunk (i%8)^(row%8). Source rows are clamped to the
   // matrix: rows past M / N only feed outputs that are never stored.
   const int lrow = lane >> 3, lkc = (lane & 7) ^ lrow;
@@ -221,13 +222,13 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(
     const int64_t ko = (int64_t)kt * 64 + lkc * 8;
 #pragma unroll
     for (int j = 0; j < NA; ++j)
-      __builtin_amdgcn_global_load_lds((const void *)(A + (int64_t)min(arow + 32 * j, M - 1) * lda + ko),
-                                       (__attribute__((address_space(3))) void *)(sa + (j * 4 + w) * 64),
+      __builtin_amdgcn_global_load_lds((const void *)(A + (int64_t)min(arow + 8 * NWV * j, M - 1) * lda + ko),
+                                       (__attribute__((address_space(3))) void *)(sa + (j * NWV + w) * 64),
                                        16, 0, 0);
 #pragma unroll
     for (int j = 0; j < NB; ++j)
-      __builtin_amdgcn_global_load_lds((const void *)(B + (int64_t)min(brow + 32 * j, N - 1) * ldb + ko),
-                                       (__attribute__((address_space(3))) void *)(sb + (j * 4 + w) * 64),
+      __builtin_amdgcn_global_load_lds((const void *)(B + (int64_t)min(brow + 8 * NWV * j, N - 1) * ldb + ko),
+                                       (__attribute__((address_space(3))) void *)(sb + (j * NWV + w) * 64),
                                        16, 0, 0);
   };
 
@@ -369,13 +370,15 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(
 // fit two blocks per CU (<= 80 KB of LDS). SwiGLU needs whole [gate|up]
 // 64-column pairs per wave (FN even).
 static int pick_dma_tile(int64_t M, int64_t N, bool swiglu, int cus) {
-  struct Cand { int fm, fn; double eff; };
-  const Cand cands[] = {{2, 2, 0.95}, {2, 3, 1.0}, {2, 4, 1.0}, {4, 4, 1.15}};
+  struct Cand { int bm, bn, fn_wave; double eff; };
+  // 128x128 / 128x192 / 128x256: 4 waves (2x2); 256x256: 8 waves (4x2) of 64x128
+  const Cand cands[] = {{128, 128, 2, 0.95}, {128, 192, 3, 1.0}, {128, 256, 4, 1.0},
+                        {256, 256, 4, 1.25}};
   int best = -1;
   double best_t = 0.0;
   for (int c = 0; c < 4; ++c) {
-    if (swiglu && (cands[c].fn & 1)) continue;
-    const int64_t bm = 64 * cands[c].fm, bn = 64 * cands[c].fn;
+    if (swiglu && (cands[c].fn_wave & 1)) continue;
+    const int64_t bm = cands[c].bm, bn = cands[c].bn;
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int64_t per_cu = (tiles + cus - 1) / cus;
     const double t = (double)per_cu * (double)(bm * bn) / cands[c].eff;
@@ -397,12 +400,13 @@ static int device_cus() {
   return cached[dev];
 }
 
-template <typename T, int EPI, int ACT, int FM, int FN>
+template <typename T, int EPI, int ACT, int FM, int FN, int WM, int WN>
 static void launch_dma(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                        int64_t ldc, const void *bias, int64_t M, int64_t N, int64_t K,
                        hipStream_t st) {
-  const int64_t nb = ((M + 64 * FM - 1) / (64 * FM)) * ((N + 64 * FN - 1) / (64 * FN));
-  gemm_dma_kernel<T, EPI, ACT, FM, FN, 2><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+  constexpr int BM = 32 * WM * FM, BN = 32 * WN * FN;
+  const int64_t nb = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  gemm_dma_kernel<T, EPI, ACT, FM, FN, 2, WM, WN><<<dim3((unsigned)nb), dim3(64 * WM * WN), 0, st>>>(
       (const T *)A, lda, (const T *)B, ldb, (T *)C, ldc, (const T *)bias, (int)M, (int)N, (int)K);
 }
 
@@ -446,10 +450,10 @@ static int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, v
     if ((M + 127) / 128 * ((N + 127) / 128) > 0x7fffffffLL)
       return set_error(TPP_E_UNSUPPORTED, "%s: too many tiles", name);
     switch (pick_dma_tile(M, N, EPI == kGSwiGLU, device_cus())) {
-    case 0: launch_dma<T, EPI, ACT, 2, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    case 1: launch_dma<T, EPI, ACT, 2, 3>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    case 2: launch_dma<T, EPI, ACT, 2, 4>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    default: launch_dma<T, EPI, ACT, 4, 4>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 0: launch_dma<T, EPI, ACT, 2, 2, 2, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 1: launch_dma<T, EPI, ACT, 2, 3, 2, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 2: launch_dma<T, EPI, ACT, 2, 4, 2, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    default: launch_dma<T, EPI, ACT, 2, 4, 4, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
     }
   } else if (vec) {
     const int64_t nb = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
