@@ -341,6 +341,23 @@ def traffic_probe(L: int, launches: int = 16):
                       "copy_bytes_each_way": src.numel() * 2}), flush=True)
 
 
+def measured_traffic(cache_len: int):
+    """HBM bytes per launch of the roofline kernel from the committed counter
+    summary (two rocprofv3 --pmc passes calibrated on a copy of known size),
+    when it was measured at this cache length; else None."""
+    import re
+    path = os.path.join(ROOT, "profiles", "attn_decode_b8_l2176_traffic.md")
+    try:
+        txt = open(path).read()
+    except OSError:
+        return None
+    b = re.search(r"^traffic_bytes_per_launch: (\d+)$", txt, re.M)
+    L = re.search(r"^traffic_cache_len: (\d+)$", txt, re.M)
+    if not b or not L or int(L.group(1)) != cache_len:
+        return None
+    return int(b.group(1))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -434,9 +451,10 @@ def main():
                                "head_dim 128, SwiGLU 3072, vocab 151936), batch 8, prefill 2048",
                    "global_batch": BATCH, "prefill_len": PREFILL, "decode_steps": K,
                    "parallelism": "single GPU"},
-        "roofline": {"kernel": "attn_decode_kernel", "bound": "hbm", "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": attn_bytes, "avg_launch_us": round(attn_us, 3),
+        "roofline": {"kernel": "attn_decode_kernel + attn_decode_merge_kernel", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(L),
+                     "bytes_per_launch": attn_bytes, "avg_launch_us": round(attn_us, 3),
                      "cache_len": L},
         "prefill": {"ms": round(prefill_s * 1e3, 3), "tok_per_s": round(BATCH * PREFILL / prefill_s, 1)},
         "kernels": kernels,

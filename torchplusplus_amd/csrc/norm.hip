@@ -38,6 +38,21 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
   const bool valid = row < M;
   const int nvec = N >> 3;
 
+  // the weight (and bias) chunks are requested together with x, so the
+  // output pass after the row reduction waits on no further memory
+  typedef typename VecT<T>::v8 V8;
+  constexpr bool kOut = (MODE == kRms || MODE == kLayer || MODE == kAddRms);
+  V8 wr[MAXV], br[MAXV];
+  if constexpr (kOut) {
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int c = j * LPR + l;
+      if (valid && c < nvec) {
+        wr[j] = *reinterpret_cast<const V8 *>(w + (int64_t)c * 8);
+        if (MODE == kLayer && b) br[j] = *reinterpret_cast<const V8 *>(b + (int64_t)c * 8);
+      }
+    }
+  }
   float v[MAXV][8];
   float sum = 0.f;
 #pragma unroll
@@ -102,19 +117,16 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
     for (int j = 0; j < MAXV; ++j) {
       const int c = j * LPR + l;
       if (c < nvec) {
-        float wv[8], o[8];
-        load8(w + (int64_t)c * 8, wv);
+        float o[8];
         if constexpr (MODE == kLayer) {
-          float bv[8];
-          if (b) load8(b + (int64_t)c * 8, bv);
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            o[i] = ((v[j][i] - mean) * scale) * wv[i];
-            if (b) o[i] += bv[i];
+            o[i] = ((v[j][i] - mean) * scale) * to_f32(wr[j][i]);
+            if (b) o[i] += to_f32(br[j][i]);
           }
         } else {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = (v[j][i] * scale) * wv[i];
+          for (int i = 0; i < 8; ++i) o[i] = (v[j][i] * scale) * to_f32(wr[j][i]);
         }
         store8(y + row * ldy + (int64_t)c * 8, o);
       }
