@@ -79,12 +79,20 @@ __device__ __forceinline__ f32x16 mfma32x32(typename VecT<T>::v8 a, typename Vec
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ int vt_swz(int d) { return (d ^ (d >> 3)) & 15; }
+// V^T tile slot of keys 4s..4s+3 for row d: within each group of four slots
+// the middle two are swapped (so the two 4-key runs one MFMA lane needs,
+// slots 4c+h and 4c+2+h, sit side by side and load as one 16-byte read), then
+// XORed with an even per-row value (keeps those pairs adjacent; 8 consecutive
+// rows hit 8 distinct 16-byte bank groups).
+__device__ __forceinline__ int vt_pos(int s, int d) {
+  const int perm = (s & ~3) | ((s & 1) << 1) | ((s >> 1) & 1);
+  return perm ^ (((d ^ (d >> 3)) & 7) << 1);
+}
 
 template <typename T, int D> struct PrefillSmem {
   typedef typename VecT<T>::v8 V8;
   V8 k[2][kKvTile * D / 8];  // [key][chunk ^ (key % (D/8))]
-  uint64_t vt[2][D * 16];    // [d][slot ^ vt_swz(d)], slot = 4 keys
+  uint64_t vt[2][D * 16];    // [d][vt_pos(slot, d)], slot = 4 keys
 };
 
 template <typename T, int D, int QG, int NW>
@@ -187,7 +195,7 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int d = vch * 8 + j;
-        sm.vt[buf][d * 16 + (vkg ^ vt_swz(d))] = (uint64_t)w0[j] | ((uint64_t)w1[j] << 16) |
+        sm.vt[buf][d * 16 + vt_pos(vkg, d)] = (uint64_t)w0[j] | ((uint64_t)w1[j] << 16) |
                                                  ((uint64_t)w2[j] << 32) |
                                                  ((uint64_t)w3[j] << 48);
       }
@@ -294,11 +302,8 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt) {
         const int d = tt * 32 + ql;
-        const int sw = vt_swz(d);
-        const uint64_t u0 = sm.vt[buf][d * 16 + ((4 * c + h) ^ sw)];
-        const uint64_t u1 = sm.vt[buf][d * 16 + ((4 * c + 2 + h) ^ sw)];
-        u32x4 raw = {(uint32_t)u0, (uint32_t)(u0 >> 32), (uint32_t)u1, (uint32_t)(u1 >> 32)};
-        const V8 a = __builtin_bit_cast(V8, raw);
+        // slots 4c+h and 4c+2+h (keys 16c+4h.. and 16c+8+4h..) in one read
+        const V8 a = *reinterpret_cast<const V8 *>(&sm.vt[buf][d * 16 + vt_pos(4 * c + h, d)]);
 #pragma unroll
         for (int g = 0; g < QG; ++g) o[g][tt] = mfma32x32<T>(a, pb[g][c], o[g][tt]);
       }
