@@ -288,6 +288,66 @@ def measure_configs():
     return out
 
 
+def cpu_configs(configs):
+    """The oracle (PyTorch CPU restatement of each reference op) timed on the
+    host cores beside every BASELINE config entry: median of 3 calls after one
+    warm-up, same shapes and dtypes (attention on a 1-sequence sample, scaled
+    to the config's batch; noted in `cpu_sample`)."""
+    import oracle
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    g = torch.Generator().manual_seed(0)
+
+    def rnd(*shape, dtype, std=1.0, mean=0.0):
+        return (mean + std * torch.randn(*shape, generator=g)).to(dtype)
+
+    def med_us(fn, reps=3):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        return ts[len(ts) // 2] * 1e6
+
+    x = rnd(4096, 1024, dtype=torch.float16)
+    w = rnd(1024, dtype=torch.float16, std=0.1, mean=1.0)
+    cos, sin = oracle.compute_rope_params(128, 1e6, 2048)
+    q1, k1 = rnd(1, 16, 2048, 128, dtype=torch.bfloat16), rnd(1, 8, 2048, 128, dtype=torch.bfloat16)
+    xl, wl, bl = (rnd(2048, 1024, dtype=torch.bfloat16), rnd(3072, 1024, dtype=torch.bfloat16, std=0.02),
+                  rnd(3072, dtype=torch.bfloat16, std=0.02))
+    qa, ka, va = (rnd(1, 2048, 16, 128, dtype=torch.bfloat16), rnd(1, 2048, 8, 128, dtype=torch.bfloat16),
+                  rnd(1, 2048, 8, 128, dtype=torch.bfloat16))
+    timings = {
+        "rmsnormFused": (lambda: oracle.rmsnorm(x, w, 1e-6), 1, "exact config"),
+        "applyLayernorm": (lambda: oracle.layernorm(x, w, 1e-6), 1, "exact config"),
+        "qkrope_apply": (lambda: oracle.qkrope(q1, k1, cos, sin), 1, "exact config"),
+        "rope_apply_": (lambda: oracle.qkrope(q1, k1, cos, sin), 1, "exact config (out of place)"),
+        "LinearSilu": (lambda: oracle.linear_act(xl, wl, bl, "silu"), 1, "exact config"),
+        "LinearGelu": (lambda: oracle.linear_act(xl, wl, bl, "gelu"), 1, "exact config"),
+        "flash_attn causal B4": (lambda: oracle.attention(qa, ka, va, causal=True), 4,
+                                 "batch 1 of 4, x4"),
+        "flash_attn causal window": (lambda: oracle.attention(qa, ka, va, causal=True, window=(511, 0)), 4,
+                                     "batch 1 of 4, x4"),
+    }
+    for K, N in ((1024, 3072), (3072, 1024)):
+        xv, wv = rnd(1, K, dtype=torch.float16), rnd(N, K, dtype=torch.float16, std=0.02)
+        timings[f"hgemv fp16 [1x{K}]"] = ((lambda xv=xv, wv=wv: oracle.gemv(xv, wv)), 1, "exact config")
+    qd = rnd(1, 1, 16, 128, dtype=torch.bfloat16)
+    kc, vc = rnd(1, 8, 4096, 128, dtype=torch.bfloat16), rnd(1, 8, 4096, 128, dtype=torch.bfloat16)
+    sl = torch.tensor([4096], dtype=torch.int32)
+    timings["attn_decode B32"] = ((lambda: oracle.decode_attention(qd, kc, vc, sl)), 32, "batch 1 of 32, x32")
+    cores = len(os.sched_getaffinity(0))
+    for e in configs:
+        for key, (fn, scale, sample) in timings.items():
+            if e["kernel"].startswith(key):
+                e["cpu_us"] = round(med_us(fn) * scale, 1)
+                e["cpu_cores"] = cores
+                e["cpu_sample"] = "oracle on the host CPU, " + sample
+                break
+
+
 def cpu_baseline(model, cfg, steps: int = 3):
     """The oracle's eager PyTorch decode (fp32 math, bf16 rounding at op
     boundaries) on this host: batch 8, synthetic 2048-position cache."""
@@ -364,7 +424,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=8)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the roofline kernel + a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -432,6 +492,8 @@ def main():
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
         cpu = cpu_baseline(model, cfg, args.cpu_steps)
+        cpu_configs(configs)
+        log("[bench] cpu config timings done")
 
     achieved = attn_bytes / attn_us / 1e3
     line = {
