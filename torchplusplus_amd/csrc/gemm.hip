@@ -240,6 +240,27 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  // bias of the wave's output columns (4 per lane per 8-column group),
+  // requested now so its latency hides under the main loop
+  typedef typename VecT<T>::v4 V4;
+  const int nw0 = n0 + wn * FN * 32; // first W row (output column before SwiGLU) of the wave
+  V4 bpre[EPI == kGBiasAct ? FN : 1][4];
+  if constexpr (EPI == kGBiasAct) {
+    const bool bias_vec = (reinterpret_cast<uintptr_t>(bias) & 7) == 0;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c0 = nw0 + j * 32 + q * 8 + (lane >> 5) * 4;
+        if (bias && bias_vec && c0 + 4 <= N) {
+          bpre[j][q] = *reinterpret_cast<const V4 *>(bias + c0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bpre[j][q][e] = (bias && c0 + e < N) ? bias[c0 + e] : (T)0.0f;
+        }
+      }
+  }
+
   const int nk = K / 64;
 #pragma unroll
   for (int p = 0; p < NST - 1; ++p)
@@ -293,8 +314,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
   __builtin_amdgcn_s_barrier(); // every wave is done reading the ring
   T *stage = reinterpret_cast<T *>(smem) + w * (FM * 32 * LDR);
   const int half = lane >> 5, ml = lane & 31;
-  const int nw0 = n0 + wn * FN * 32; // first W row (output column before SwiGLU) of the wave
-  const bool bias_vec = (reinterpret_cast<uintptr_t>(bias) & 7) == 0;
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     if constexpr (EPI == kGSwiGLU) {
@@ -305,17 +324,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
       const int nl = j * 32 + q * 8 + half * 4; // wave-local W column of register 4q
       float bv[4] = {0.f, 0.f, 0.f, 0.f};
       if constexpr (EPI == kGBiasAct) {
-        if (bias) {
-          const int c0 = nw0 + nl;
-          if (bias_vec && c0 + 4 <= N) { // one 8-byte load for the 4 columns
-            const typename VecT<T>::v4 b4 = *reinterpret_cast<const typename VecT<T>::v4 *>(bias + c0);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) bv[e] = to_f32(b4[e]);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) bv[e] = c0 + e < N ? to_f32(bias[c0 + e]) : 0.f;
-          }
-        }
+        for (int e = 0; e < 4; ++e) bv[e] = to_f32(bpre[j][q][e]);
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
