@@ -183,6 +183,21 @@ def test_gemv_argmax_lm_head(dev, bsz, n):
     assert len(only) == 1 and torch.equal(only[0], idx)
 
 
+@pytest.mark.parametrize("bsz,n,k,norm", [(16, 40001, 512, True), (1, 33000, 256, False),
+                                           (5, 50000, 768, True), (8, 36000, 1024, False)])
+def test_gemv_wide_path(dev, bsz, n, k, norm):
+    """>= 2048 row tiles with K % 256 == 0 run the whole-K-per-wave kernel:
+    ragged last tile, every chunk count, with and without the input norm."""
+    x, w, _ = _mk(bsz, n, k, torch.bfloat16, seed=23)
+    nw = (1 + 0.1 * torch.randn(k, generator=torch.Generator().manual_seed(24))).bfloat16()
+    idx, logits = ext().gemv_argmax(x.to(dev), w.to(dev), nw.to(dev) if norm else None, 1e-6, True)
+    xin = oracle.rmsnorm(x, nw, 1e-6) if norm else x
+    close(logits, oracle.linear_act(xin, w), what=f"wide gemv {bsz}x{n}x{k}")
+    assert torch.equal(idx.cpu(), torch.argmax(logits.cpu().float(), dim=-1))
+    y = ext().gemv(x.to(dev), w.to(dev))
+    close(y, oracle.gemv(x, w), what=f"wide plain gemv {bsz}x{n}x{k}")
+
+
 @pytest.mark.parametrize("n", [5000, 40000])
 def test_greedy_step_tail(dev, n):
     """argmax -> ids, next embedding gathered into the residual row, and the

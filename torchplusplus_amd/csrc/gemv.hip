@@ -451,6 +451,177 @@ static bool gemv_vec_ok(const GemvArgs &a) {
          (a.norm_w == nullptr || aligned16(a.norm_w)) && a.NB <= 16;
 }
 
+// ---------------------------------------------------------------------------
+// Wide GEMV (many row tiles, K in {256, 512, 768, 1024}, plain epilogue: the
+// lm_head). Every
+// wave owns whole 16-row tiles, so the stream has no cross-wave reduction and
+// no barrier. Weights go HBM -> LDS by LDS-DMA in 16-row x 256-k chunks
+// (each row's 512 bytes read by 32 consecutive lanes: whole 128-byte lines)
+// through a per-wave ring of kWideRing chunks; MFMA operands are read back
+// with ds_read_b128 (16-byte units XOR-swizzled by row % 8: conflict-free);
+// the (normalised) input stays in VGPRs as the A operand for the whole K.
+constexpr int kWideRing = 4;          // chunks per wave ring (3 in flight)
+constexpr int kWideBlocks = 256;      // one 4-wave block per CU
+constexpr int64_t kWideMinTiles = 2048;
+
+template <int N> __device__ __forceinline__ void gemv_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <typename T, bool NORM, int KC>
+__global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tiles) {
+  typedef typename VecT<T>::v8 V8;
+  __shared__ V8 ring[4][kWideRing][16 * 32]; // [wave][slot][row * 32 + (unit ^ row % 8)]
+  __shared__ float s_inv[16];
+  __shared__ float s_bv[4][16];
+  __shared__ int s_bi[4][16];
+  const int lane = lane_id(), w = wave_id();
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t K = a.K, N = a.N;
+  const T *X = (const T *)a.x;
+  const T *W = (const T *)a.W;
+  const int64_t wg = (int64_t)blockIdx.x * 4 + w, nwg = (int64_t)gridDim.x * 4;
+  // this wave's tiles: wg, wg + nwg, ...; its chunk stream n = tile_i * KC + c
+  const int64_t my_tiles = wg < tiles ? (tiles - 1 - wg) / nwg + 1 : 0;
+  const int64_t nchunks = my_tiles * KC;
+
+  // DMA of chunk n into ring slot n % kWideRing. Instruction j covers rows
+  // 2j, 2j+1; lane i lands at slot offset i and so fetches unit
+  // (i % 32) ^ (row % 8) of row 2j + i / 32. Past the end of the stream the
+  // last chunk is fetched again, so every wave keeps the same issue pattern.
+  const int drow = lane >> 5, dpos = lane & 31;
+  auto issue = [&](int64_t n) {
+    const int64_t nn = n < nchunks ? n : nchunks - 1;
+    const int64_t tile = wg + (nn / KC) * nwg;
+    const int c = (int)(nn % KC);
+    V8 *dst = ring[w][(int)(n % kWideRing)];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = 2 * j + drow;
+      const int64_t wr = tile * 16 + row < N ? tile * 16 + row : N - 1;
+      const int64_t k = (int64_t)c * 256 + (dpos ^ (row & 7)) * 8;
+      __builtin_amdgcn_global_load_lds((const void *)(W + wr * K + k),
+                                       (__attribute__((address_space(3))) void *)(dst + j * 64),
+                                       16, 0, 0);
+    }
+  };
+  if (nchunks > 0) {
+#pragma unroll
+    for (int p = 0; p < kWideRing - 1; ++p) issue(p);
+  }
+
+  // input rows (<= 16) as A fragments for all K: step u covers k = 32u + 8g
+  if constexpr (NORM) {
+    for (int row = w; row < a.NB; row += 4) {
+      const T *xp = X + row * a.ldx;
+      float ss = 0.f;
+      for (int64_t c = (int64_t)lane * 8; c < K; c += 64 * 8) {
+        float v[8];
+        load8(xp + c, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) s_inv[row] = rsqrtf(ss / (float)K + a.eps);
+    }
+    __syncthreads();
+  }
+  const bool xok = r < a.NB;
+  const T *xr = X + (xok ? r : 0) * a.ldx;
+  V8 xa[KC * 8];
+#pragma unroll
+  for (int u = 0; u < KC * 8; ++u) {
+    const int64_t c = (int64_t)u * 32 + g * 8;
+    const bool ok = c < K && xok;
+    xa[u] = ld16(xr + c, ok);
+    if constexpr (NORM) {
+      if (ok) {
+        float nv[8];
+        load8((const T *)a.norm_w + c, nv);
+        const float inv = s_inv[r];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xa[u][i] = from_f32<T>((to_f32(xa[u][i]) * inv) * nv[i]);
+      }
+    }
+  }
+
+  float bv[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  int bi[4] = {0x7fffffff, 0x7fffffff, 0x7fffffff, 0x7fffffff};
+  T *Y = (T *)a.y;
+  for (int64_t ti = 0; ti < my_tiles; ++ti) {
+    const int64_t tile = wg + ti * nwg;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int64_t n = ti * KC + c;
+      gemv_wait_vmcnt<(kWideRing - 2) * 8>(); // chunk n landed (own DMA)
+      const V8 *src = ring[w][(int)(n % kWideRing)];
+      V8 b[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) b[u] = src[r * 32 + ((u * 4 + g) ^ (r & 7))];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = mfma16<T>(xa[c * 8 + u], b[u], acc);
+      // the slot read last is refilled only after those reads completed
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      issue(n + kWideRing - 1);
+    }
+    // D layout of 16x16x32: lane -> weight row tile*16 + r, rows b = 4g + i
+    const int64_t col = tile * 16 + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = 4 * g + i;
+      const T yv = from_f32<T>(acc[i]);
+      if (col < N && b < a.NB) {
+        if (Y) Y[(int64_t)b * a.ldy + col] = yv;
+        const float v = to_f32(yv);
+        if (am_better(v, (int)col, bv[i], bi[i])) bv[i] = v, bi[i] = (int)col;
+      }
+    }
+  }
+  gemv_wait_vmcnt<0>(); // drain the refetches before the wave exits
+  if (!a.am_val) return;
+  // argmax over the 16 columns of each lane group, then over the 4 waves
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int sh = 1; sh < 16; sh <<= 1) {
+      const float ov = __shfl_xor(bv[i], sh, kWave);
+      const int oi = __shfl_xor(bi[i], sh, kWave);
+      if (am_better(ov, oi, bv[i], bi[i])) bv[i] = ov, bi[i] = oi;
+    }
+    if (r == 0) {
+      s_bv[w][4 * g + i] = bv[i];
+      s_bi[w][4 * g + i] = bi[i];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < (unsigned)a.NB) {
+    const int b = threadIdx.x;
+    float v = s_bv[0][b];
+    int ix = s_bi[0][b];
+    for (int ww = 1; ww < 4; ++ww)
+      if (am_better(s_bv[ww][b], s_bi[ww][b], v, ix)) v = s_bv[ww][b], ix = s_bi[ww][b];
+    a.am_val[(int64_t)blockIdx.x * a.NB + b] = v;
+    a.am_idx[(int64_t)blockIdx.x * a.NB + b] = ix;
+  }
+}
+
+template <typename T, bool NORM>
+static bool launch_wide(const GemvArgs &a, hipStream_t st) {
+  const int64_t tiles = (a.N + 15) / 16;
+  if (tiles < kWideMinTiles || a.K > 1024 || a.K % 256 != 0) return false;
+  const int kc = (int)((a.K + 255) / 256);
+  const dim3 grid(kWideBlocks), block(256);
+  switch (kc) {
+  case 1: gemv_wide_kernel<T, NORM, 1><<<grid, block, 0, st>>>(a, tiles); break;
+  case 2: gemv_wide_kernel<T, NORM, 2><<<grid, block, 0, st>>>(a, tiles); break;
+  case 3: gemv_wide_kernel<T, NORM, 3><<<grid, block, 0, st>>>(a, tiles); break;
+  default: gemv_wide_kernel<T, NORM, 4><<<grid, block, 0, st>>>(a, tiles); break;
+  }
+  return true;
+}
+
 template <typename T, int EPI, int ACT, bool NORM>
 static int launch_gemv(GemvArgs a, hipStream_t st, const char *name) {
   const int64_t NO = (EPI == kEpiSwiGLU) ? a.N / 2 : a.N;
@@ -462,6 +633,9 @@ static int launch_gemv(GemvArgs a, hipStream_t st, const char *name) {
   }
   const int64_t tiles = (EPI == kEpiSwiGLU) ? (a.N / 64) * 2 : (a.N + 15) / 16;
   if (tiles > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: N too large", name);
+  if constexpr (EPI == kEpiPlain) {
+    if (launch_wide<T, NORM>(a, st)) return check_launch(name);
+  }
   // SwiGLU holds two W tiles per lane: cap its block at 8 waves (256 VGPRs)
   constexpr int MAXW = EPI == kEpiSwiGLU ? 8 : kGemvMaxWaves;
   int64_t nw = (a.K + kGemvWaveK - 1) / kGemvWaveK;
@@ -570,6 +744,7 @@ static int gemv_argmax_launch(const char *name, const void *x, const void *norm_
   if (N > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: N too large", name);
   const int64_t tiles = (N + 15) / 16;
   nparts = (int)(tiles < kGemvMaxBlocks ? tiles : kGemvMaxBlocks);
+  if (tiles >= kWideMinTiles && K <= 1024 && K % 256 == 0) nparts = kWideBlocks;
   const size_t need = tpp_gemv_argmax_workspace_size(B, N);
   if (!workspace || ws_bytes < need || !aligned16(workspace))
     return set_error(TPP_E_WORKSPACE, "%s: workspace of %zu bytes required", name, need);
