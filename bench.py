@@ -429,8 +429,9 @@ def main():
                     help="only run the roofline kernel + a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the decode path shards by KV head "
-              "across GPUs by design, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only; across GPUs the decode path would "
+              "shard by KV head (attention) and by columns/rows (projections), which is not "
+              "built here. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     if args.traffic_probe:
