@@ -418,6 +418,38 @@ def measured_traffic(cache_len: int):
     return int(b.group(1))
 
 
+def kernel_probe(name: str, reps: int = 5):
+    """Counter runs (rocprofv3 --pmc ...) of one BASELINE config kernel:
+    `gemm` = Linear+SiLU [2048x1024]x[3072x1024]^T + bias and the prefill
+    qkv GEMM [16384x1024]x[4096x1024]^T; `attn_prefill` = causal flash
+    attention B4 S2048 16/8 d128. `reps` launches each, no timing."""
+    from torchplusplus_amd._native import ext
+
+    C = ext()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    if name == "gemm":
+        x = torch.randn(2048, 1024, generator=g, device=dev).bfloat16()
+        w = (0.02 * torch.randn(3072, 1024, generator=g, device=dev)).bfloat16()
+        b = (0.02 * torch.randn(3072, generator=g, device=dev)).bfloat16()
+        xp = torch.randn(16384, 1024, generator=g, device=dev).bfloat16()
+        wp = (0.02 * torch.randn(4096, 1024, generator=g, device=dev)).bfloat16()
+        for _ in range(reps):
+            C.LinearSilu(x, w, b)
+        for _ in range(reps):
+            C.linear(xp, wp, None, 0)
+    elif name == "attn_prefill":
+        q = torch.randn(4, 2048, 16, 128, generator=g, device=dev).bfloat16()
+        k = torch.randn(4, 2048, 8, 128, generator=g, device=dev).bfloat16()
+        v = torch.randn(4, 2048, 8, 128, generator=g, device=dev).bfloat16()
+        for _ in range(reps):
+            C.flash_attn_func(q, k, v, True, -1, -1, 0.0)
+    else:
+        raise SystemExit(f"unknown probe {name}")
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": name, "reps": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -427,6 +459,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=8)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the roofline kernel + a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--kernel-probe", choices=["gemm", "attn_prefill"],
+                    help="only launch one config's kernels a few times (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; across GPUs the decode path would "
@@ -434,6 +468,11 @@ def main():
               "built here. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
+    if args.kernel_probe:
+        torch.cuda.set_device(0)
+        with torch.inference_mode():
+            kernel_probe(args.kernel_probe)
+        return
     if args.traffic_probe:
         torch.cuda.set_device(0)
         with torch.inference_mode():

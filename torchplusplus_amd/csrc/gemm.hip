@@ -29,6 +29,18 @@ namespace tpp {
 enum GemmEpi { kGPlain = 0, kGBiasAct = 1, kGSwiGLU = 2 };
 
 constexpr int kBM = 128, kBN = 128, kBK = 64;
+
+// LDS tiles hold 128-byte rows of eight 16-byte chunks; chunk c of row r is
+// stored at position c ^ swz(r). A ds_read_b128 serves 16 lanes (16 rows of
+// one fragment) per cycle from 16 distinct 16-byte bank groups only if those
+// rows land in different groups: rows r and r+1 already differ in the row's
+// half of the 256-byte bank space, so the XOR uses row bits 1..3 (bits 0..2
+// would put rows r and r+8 on the same banks: a 2-way conflict on every read).
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
+// K-tile depth and ring stages of the 256x256 tile (64 KB per stage at BK 64;
+// a 4-stage ring of BK 32 tiles measured no faster)
+constexpr int kBigBK = 64, kBigNST = 2;
 // below this many outputs the register-staged kernel's smaller LDS footprint
 // (several blocks per CU) wins over the deeper DMA ring
 constexpr int64_t kDmaMinMN = 256 * 128 * 128;
@@ -94,8 +106,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
-      sA[buf][row * 8 + (kc ^ (row & 7))] = ra[i];
-      sB[buf][row * 8 + (kc ^ (row & 7))] = rb[i];
+      sA[buf][row * 8 + (kc ^ swz(row))] = ra[i];
+      sB[buf][row * 8 + (kc ^ swz(row))] = rb[i];
     }
   };
 
@@ -121,9 +133,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int row = wm * 64 + i * 32 + (lane & 31);
-        af[i] = sA[buf][row * 8 + (kc ^ (row & 7))];
+        af[i] = sA[buf][row * 8 + (kc ^ swz(row))];
         const int col = wn * 64 + i * 32 + (lane & 31);
-        bfr[i] = sB[buf][col * 8 + (kc ^ (col & 7))];
+        bfr[i] = sB[buf][col * 8 + (kc ^ swz(col))];
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -182,7 +194,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 // fewer tiles than CUs the 128-row tiles (two blocks per CU with a 2-stage
 // ring) win.
 // An LDS-DMA instruction writes lane i's 16 bytes at base + 16*i; lane i of
-// a row group therefore fetches the 16-byte chunk kc = (i%8) ^ (row%8), which
+// a row group therefore fetches the 16-byte chunk kc = (i%8) ^ swz(row), which
 // lands the tile in the same XOR-swizzled layout the fragment reads expect.
 // Waits are explicit (s_waitcnt vmcnt / lgkmcnt + s_barrier): a fenced
 // __syncthreads() would drain every DMA in flight at each K step.
@@ -192,14 +204,25 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-template <typename T, int EPI, int ACT, int FM, int FN, int NST, int WM, int WN>
+template <int BK> __device__ __forceinline__ int swzk(int row) {
+  // BK = 64: 128-byte rows, two per 256-byte bank space; BK = 32: 64-byte rows,
+  // four per bank space. The XOR uses the row bits above those, so the 16
+  // rows one ds_read_b128 cycle serves hit 16 distinct 16-byte bank groups.
+  if constexpr (BK == 64) return (row >> 1) & 7;
+  else return (row >> 2) & 3;
+}
+
+template <typename T, int EPI, int ACT, int FM, int FN, int NST, int WM, int WN, int BK>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
     const T *__restrict__ A, int64_t lda, const T *__restrict__ B, int64_t ldb,
     T *__restrict__ C, int64_t ldc, const T *__restrict__ bias, int M, int N, int K) {
   typedef typename VecT<T>::v8 V8;
   constexpr int BM = 32 * WM * FM, BN = 32 * WN * FN, NWV = WM * WN;
-  constexpr int STG = (BM + BN) * 8; // 16-byte slots per stage
-  constexpr int NA = BM / 8 / NWV, NB = BN / 8 / NWV; // DMA instructions per wave per stage
+  constexpr int CPR = BK / 8;                // 16-byte chunks per tile row
+  constexpr int RPI = 64 / CPR;              // tile rows per DMA instruction
+  constexpr int STG = (BM + BN) * CPR;       // 16-byte slots per stage
+  constexpr int NA = BM / RPI / NWV, NB = BN / RPI / NWV; // DMA instructions per wave per stage
+  static_assert(NA * RPI * NWV == BM && NB * RPI * NWV == BN, "tile rows per wave");
   // the epilogue's staging tile reuses the ring
   constexpr int OWS = (EPI == kGSwiGLU) ? FN * 16 : FN * 32;
   constexpr int RING = NST * STG, OUTS = NWV * FM * 32 * (OWS + 8) * (int)sizeof(T) / 16;
@@ -212,22 +235,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w / WN, wn = w % WN;
 
-  // DMA instruction j of wave w covers tile rows (NWV*j + w)*8 .. +7; lane i
-  // fetches row +i/8, chunk (i%8)^(row%8). Source rows are clamped to the
-  // matrix: rows past M / N only feed outputs that are never stored.
-  const int lrow = lane >> 3, lkc = (lane & 7) ^ lrow;
-  const int arow = m0 + w * 8 + lrow, brow = n0 + w * 8 + lrow;
+  // DMA instruction j of wave w covers tile rows (NWV*j + w)*RPI .. +RPI-1;
+  // lane i fetches row +i/CPR, chunk (i%CPR)^swzk(row). swzk(row) depends on
+  // w and i only (NWV is even). Source rows are clamped to the matrix: rows
+  // past M / N only feed outputs that are never stored.
+  const int lrow = lane / CPR, lkc = (lane % CPR) ^ swzk<BK>(RPI * w + lrow);
+  const int arow = m0 + w * RPI + lrow, brow = n0 + w * RPI + lrow;
   auto issue = [&](int stage, int kt) {
-    V8 *sa = smem + stage * STG, *sb = sa + BM * 8;
-    const int64_t ko = (int64_t)kt * 64 + lkc * 8;
+    V8 *sa = smem + stage * STG, *sb = sa + BM * CPR;
+    const int64_t ko = (int64_t)kt * BK + lkc * 8;
 #pragma unroll
     for (int j = 0; j < NA; ++j)
-      __builtin_amdgcn_global_load_lds((const void *)(A + (int64_t)min(arow + 8 * NWV * j, M - 1) * lda + ko),
+      __builtin_amdgcn_global_load_lds((const void *)(A + (int64_t)min(arow + RPI * NWV * j, M - 1) * lda + ko),
                                        (__attribute__((address_space(3))) void *)(sa + (j * NWV + w) * 64),
                                        16, 0, 0);
 #pragma unroll
     for (int j = 0; j < NB; ++j)
-      __builtin_amdgcn_global_load_lds((const void *)(B + (int64_t)min(brow + 8 * NWV * j, N - 1) * ldb + ko),
+      __builtin_amdgcn_global_load_lds((const void *)(B + (int64_t)min(brow + RPI * NWV * j, N - 1) * ldb + ko),
                                        (__attribute__((address_space(3))) void *)(sb + (j * NWV + w) * 64),
                                        16, 0, 0);
   };
@@ -261,7 +285,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
       }
   }
 
-  const int nk = K / 64;
+  const int nk = K / BK;
 #pragma unroll
   for (int p = 0; p < NST - 1; ++p)
     if (p < nk) issue(p, p);
@@ -271,28 +295,32 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
     if constexpr (NST == 2) {
       wait_vmcnt<0>();
     } else {
-      if (kt + 1 < nk)
+      // tiles kt+1 .. kt+NST-2 may still be in flight (fewer near the end)
+      const int ahead = nk - 1 - kt < NST - 2 ? nk - 1 - kt : NST - 2;
+      if (ahead >= NST - 2)
         wait_vmcnt<(NST - 2) * (NA + NB)>();
+      else if (NST > 3 && ahead == 1)
+        wait_vmcnt<(NA + NB)>();
       else
         wait_vmcnt<0>();
     }
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
     if (kt + NST - 1 < nk) issue((kt + NST - 1) % NST, kt + NST - 1);
-    const V8 *sa = smem + (kt % NST) * STG, *sb = sa + BM * 8;
+    const V8 *sa = smem + (kt % NST) * STG, *sb = sa + BM * CPR;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < BK / 16; ++ks) {
       const int kc = ks * 2 + (lane >> 5);
       V8 af[FM], bfr[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int row = wm * FM * 32 + i * 32 + (lane & 31);
-        af[i] = sa[row * 8 + (kc ^ (row & 7))];
+        af[i] = sa[row * CPR + (kc ^ swzk<BK>(row))];
       }
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int col = wn * FN * 32 + j * 32 + (lane & 31);
-        bfr[j] = sb[col * 8 + (kc ^ (col & 7))];
+        bfr[j] = sb[col * CPR + (kc ^ swzk<BK>(col))];
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -350,15 +378,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
   wait_lgkmcnt0();
   // rows of the wave tile: OW/8 lanes per row, 16 bytes each; RPI rows per
   // pass (with OW = 96, lanes 60..63 idle)
-  constexpr int LPR = OW / 8, RPI = 64 / LPR;
+  constexpr int LPR = OW / 8, OPR = 64 / LPR; // output rows per pass
   const int oc0 = (EPI == kGSwiGLU) ? nw0 / 2 : nw0;
   const int NO = (EPI == kGSwiGLU) ? N / 2 : N;
   const int rr = lane / LPR, cc = (lane % LPR) * 8;
   const bool vec_ok = (ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
 #pragma unroll
-  for (int r0 = 0; r0 < FM * 32; r0 += RPI) {
+  for (int r0 = 0; r0 < FM * 32; r0 += OPR) {
     const int rl = r0 + rr;
-    if (rr >= RPI || rl >= FM * 32) continue;
+    if (rr >= OPR || rl >= FM * 32) continue;
     const int row = m0 + wm * FM * 32 + rl;
     const typename VecT<T>::v8 v =
         *reinterpret_cast<const typename VecT<T>::v8 *>(stage + rl * LDR + cc);
@@ -410,13 +438,13 @@ static int device_cus() {
   return cached[dev];
 }
 
-template <typename T, int EPI, int ACT, int FM, int FN, int WM, int WN>
+template <typename T, int EPI, int ACT, int FM, int FN, int WM, int WN, int BK, int NST>
 static void launch_dma(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                        int64_t ldc, const void *bias, int64_t M, int64_t N, int64_t K,
                        hipStream_t st) {
   constexpr int BM = 32 * WM * FM, BN = 32 * WN * FN;
   const int64_t nb = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  gemm_dma_kernel<T, EPI, ACT, FM, FN, 2, WM, WN><<<dim3((unsigned)nb), dim3(64 * WM * WN), 0, st>>>(
+  gemm_dma_kernel<T, EPI, ACT, FM, FN, NST, WM, WN, BK><<<dim3((unsigned)nb), dim3(64 * WM * WN), 0, st>>>(
       (const T *)A, lda, (const T *)B, ldb, (T *)C, ldc, (const T *)bias, (int)M, (int)N, (int)K);
 }
 
@@ -460,10 +488,10 @@ static int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, v
     if ((M + 127) / 128 * ((N + 127) / 128) > 0x7fffffffLL)
       return set_error(TPP_E_UNSUPPORTED, "%s: too many tiles", name);
     switch (pick_dma_tile(M, N, EPI == kGSwiGLU, device_cus())) {
-    case 0: launch_dma<T, EPI, ACT, 2, 2, 2, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    case 1: launch_dma<T, EPI, ACT, 2, 3, 2, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    case 2: launch_dma<T, EPI, ACT, 2, 4, 2, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    default: launch_dma<T, EPI, ACT, 2, 4, 4, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 0: launch_dma<T, EPI, ACT, 2, 2, 2, 2, 64, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 1: launch_dma<T, EPI, ACT, 2, 3, 2, 2, 64, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 2: launch_dma<T, EPI, ACT, 2, 4, 2, 2, 64, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    default: launch_dma<T, EPI, ACT, 2, 4, 4, 2, kBigBK, kBigNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
     }
   } else if (vec) {
     const int64_t nb = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);

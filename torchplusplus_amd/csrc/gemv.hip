@@ -458,7 +458,8 @@ static bool gemv_vec_ok(const GemvArgs &a) {
 // no barrier. Weights go HBM -> LDS by LDS-DMA in 16-row x 256-k chunks
 // (each row's 512 bytes read by 32 consecutive lanes: whole 128-byte lines)
 // through a per-wave ring of kWideRing chunks; MFMA operands are read back
-// with ds_read_b128 (16-byte units XOR-swizzled by row % 8: conflict-free);
+// with ds_read_b128 (16-byte unit u of row r stored at u ^ r: the 16 rows a
+// read serves per cycle then sit in 16 distinct 16-byte bank groups);
 // the (normalised) input stays in VGPRs as the A operand for the whole K.
 constexpr int kWideRing = 4;          // chunks per wave ring (3 in flight)
 constexpr int kWideBlocks = 256;      // one 4-wave block per CU
@@ -472,7 +473,7 @@ template <int N> __device__ __forceinline__ void gemv_wait_vmcnt() {
 template <typename T, bool NORM, int KC>
 __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tiles) {
   typedef typename VecT<T>::v8 V8;
-  __shared__ V8 ring[4][kWideRing][16 * 32]; // [wave][slot][row * 32 + (unit ^ row % 8)]
+  __shared__ V8 ring[4][kWideRing][16 * 32]; // [wave][slot][row * 32 + (unit ^ row)]
   __shared__ float s_inv[16];
   __shared__ float s_bv[4][16];
   __shared__ int s_bi[4][16];
@@ -488,7 +489,7 @@ __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tile
 
   // DMA of chunk n into ring slot n % kWideRing. Instruction j covers rows
   // 2j, 2j+1; lane i lands at slot offset i and so fetches unit
-  // (i % 32) ^ (row % 8) of row 2j + i / 32. Past the end of the stream the
+  // (i % 32) ^ row of row 2j + i / 32. Past the end of the stream the
   // last chunk is fetched again, so every wave keeps the same issue pattern.
   const int drow = lane >> 5, dpos = lane & 31;
   auto issue = [&](int64_t n) {
@@ -500,7 +501,7 @@ __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tile
     for (int j = 0; j < 8; ++j) {
       const int row = 2 * j + drow;
       const int64_t wr = tile * 16 + row < N ? tile * 16 + row : N - 1;
-      const int64_t k = (int64_t)c * 256 + (dpos ^ (row & 7)) * 8;
+      const int64_t k = (int64_t)c * 256 + (dpos ^ row) * 8;
       __builtin_amdgcn_global_load_lds((const void *)(W + wr * K + k),
                                        (__attribute__((address_space(3))) void *)(dst + j * 64),
                                        16, 0, 0);
@@ -559,7 +560,7 @@ __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tile
       const V8 *src = ring[w][(int)(n % kWideRing)];
       V8 b[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) b[u] = src[r * 32 + ((u * 4 + g) ^ (r & 7))];
+      for (int u = 0; u < 8; ++u) b[u] = src[r * 32 + ((u * 4 + g) ^ r)];
 #pragma unroll
       for (int u = 0; u < 8; ++u) acc = mfma16<T>(xa[c * 8 + u], b[u], acc);
       // the slot read last is refilled only after those reads completed
