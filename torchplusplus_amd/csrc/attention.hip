@@ -79,20 +79,23 @@ __device__ __forceinline__ f32x16 mfma32x32(typename VecT<T>::v8 a, typename Vec
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// V^T tile slot of keys 4s..4s+3 for row d: within each group of four slots
-// the middle two are swapped (so the two 4-key runs one MFMA lane needs,
-// slots 4c+h and 4c+2+h, sit side by side and load as one 16-byte read), then
-// XORed with an even per-row value (keeps those pairs adjacent; 8 consecutive
-// rows hit 8 distinct 16-byte bank groups).
-__device__ __forceinline__ int vt_pos(int s, int d) {
-  const int perm = (s & ~3) | ((s & 1) << 1) | ((s >> 1) & 1);
-  return perm ^ (((d ^ (d >> 3)) & 7) << 1);
+// V tiles are stored row-major like K ([key][16-byte unit]) and read as
+// MFMA operands with ds_read_b64_tr_b16, whose 16-lane groups return lane
+// 4a+b the b-th 16-bit element of the words lanes a, a+4, a+8, a+12 point at:
+// pointing lane a'+4c' at V[k0 + c'][d0 + 4a'] gives lane l of the group
+// V[k0 + 0..3][d0 + l]. Unit u of key row r is stored at u ^ vswz(r): the
+// 32 lanes one read cycle serves (4 keys x 32 columns) then hit distinct
+// banks (D = 128: 256-byte rows, XOR 4*(r%4); D = 64: 128-byte rows, two
+// per bank row, XOR 4*((r/2)%2)).
+template <int D> __device__ __forceinline__ int vswz(int r) {
+  if constexpr (D == 128) return 4 * (r & 3);
+  else return 4 * ((r >> 1) & 1);
 }
 
 template <typename T, int D> struct PrefillSmem {
   typedef typename VecT<T>::v8 V8;
   V8 k[2][kKvTile * D / 8];  // [key][chunk ^ (key % (D/8))]
-  uint64_t vt[2][D * 16];    // [d][vt_pos(slot, d)], slot = 4 keys
+  V8 v[2][kKvTile * D / 8];  // [key][chunk ^ vswz(key)]
 };
 
 template <typename T, int D, int QG, int NW>
@@ -153,52 +156,26 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
                       : zero;
   }
 
-  // K tiles go HBM/L2 -> LDS by LDS-DMA (no staging registers): instruction
-  // i of wave w fills 64 slots = 64/CPR keys; lane l fetches the chunk that
-  // lands in its slot, chunk (l % CPR) ^ (key % CPR). Keys past Sk are
-  // clamped to Sk-1 (finite data; those scores are masked on the edge tile).
-  // V^T tiles are transposed through VGPRs.
+  // K and V tiles go HBM/L2 -> LDS by LDS-DMA (no staging registers):
+  // instruction i of wave w fills 64 slots = 64/CPR keys; lane l fetches the
+  // chunk that lands in its slot. Keys past Sk are clamped to Sk-1 (finite
+  // data; those scores are masked, so their P is 0, on the edge tile).
   constexpr int KPI = 64 / CPR;                 // keys per DMA instruction
   constexpr int KDMA = kKvTile / KPI / NW;      // DMA instructions per wave per tile
   const int dkey = lane / CPR, dslot = lane % CPR;
-  V8 rv[4];
-  const bool vthread = tid < 16 * CPR;
-  const int vkg = tid / CPR, vch = tid % CPR;
   auto gload = [&](int t, int buf) {
     const int kb = t * kKvTile;
 #pragma unroll
     for (int i = 0; i < KDMA; ++i) {
       const int key0 = (i * NW + w) * KPI; // first key of the instruction
-      const int key = key0 + dkey, ch = dslot ^ (key & (CPR - 1));
+      const int key = key0 + dkey;
       const int kk = min(kb + key, p.Sk - 1);
       __builtin_amdgcn_global_load_lds(
-          (const void *)(kp + (int64_t)kk * p.k_ss + ch * 8),
+          (const void *)(kp + (int64_t)kk * p.k_ss + (dslot ^ (key & (CPR - 1))) * 8),
           (__attribute__((address_space(3))) void *)&sm.k[buf][key0 * CPR], 16, 0, 0);
-    }
-    if (vthread) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kk = kb + vkg * 4 + i;
-        rv[i] = kk < p.Sk ? *reinterpret_cast<const V8 *>(vp + (int64_t)kk * p.v_ss + vch * 8)
-                          : zero;
-      }
-    }
-  };
-  auto sstore = [&](int buf) {
-    if (vthread) {
-      // Whole-vector bit casts: hipcc (clang 22) miscompiles a bit cast of a
-      // single __bf16 ext-vector element into a read of element 0.
-      const u16x8 w0 = __builtin_bit_cast(u16x8, rv[0]);
-      const u16x8 w1 = __builtin_bit_cast(u16x8, rv[1]);
-      const u16x8 w2 = __builtin_bit_cast(u16x8, rv[2]);
-      const u16x8 w3 = __builtin_bit_cast(u16x8, rv[3]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int d = vch * 8 + j;
-        sm.vt[buf][d * 16 + vt_pos(vkg, d)] = (uint64_t)w0[j] | ((uint64_t)w1[j] << 16) |
-                                                 ((uint64_t)w2[j] << 32) |
-                                                 ((uint64_t)w3[j] << 48);
-      }
+      __builtin_amdgcn_global_load_lds(
+          (const void *)(vp + (int64_t)kk * p.v_ss + (dslot ^ vswz<D>(key)) * 8),
+          (__attribute__((address_space(3))) void *)&sm.v[buf][key0 * CPR], 16, 0, 0);
     }
   };
 
@@ -213,11 +190,8 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
 #pragma unroll
   for (int g = 0; g < QG; ++g) m_run[g] = -INFINITY, l_run[g] = 0.f;
 
-  if (t_begin < t_end) {
-    gload(t_begin, 0);
-    sstore(0);
-  }
-  __syncthreads(); // (its fence also drains the K DMA)
+  if (t_begin < t_end) gload(t_begin, 0);
+  __syncthreads(); // (its fence also drains the DMA)
   for (int t = t_begin; t < t_end; ++t) {
     const int buf = (t - t_begin) & 1;
     if (t + 1 < t_end) gload(t + 1, buf ^ 1);
@@ -297,18 +271,32 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
         for (int j = 0; j < 8; ++j) pb[g][c][j] = from_f32<T>(s[g][c >> 1][(c & 1) * 8 + j]);
     }
 
+    // O^T += V^T P^T: the A operand of 16-key step c for lane half h holds
+    // keys 16c + 4h + 0..3 (first read) and 16c + 8 + 4h + 0..3 (second), the
+    // key order of the score registers (P stays the B operand unchanged).
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const int grp = lane >> 4, a4 = lane & 3, c4 = (lane >> 2) & 3;
+    const __attribute__((address_space(3))) char *vbase =
+        (const __attribute__((address_space(3))) char *)&sm.v[buf][0];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
+      const int key1 = 16 * c + 4 * (grp >> 1) + c4, key2 = key1 + 8;
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt) {
-        const int d = tt * 32 + ql;
-        // slots 4c+h and 4c+2+h (keys 16c+4h.. and 16c+8+4h..) in one read
-        const V8 a = *reinterpret_cast<const V8 *>(&sm.vt[buf][d * 16 + vt_pos(4 * c + h, d)]);
+        const int d0 = tt * 32 + 16 * (grp & 1) + 4 * a4; // this lane's 4 columns
+        const int o1 = key1 * D * 2 + (((d0 >> 3) ^ vswz<D>(key1)) << 4) + ((d0 & 7) << 1);
+        const int o2 = key2 * D * 2 + (((d0 >> 3) ^ vswz<D>(key2)) << 4) + ((d0 & 7) << 1);
+        const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4 *)(vbase + o1));
+        const s16x4 r2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4 *)(vbase + o2));
+        const s16x8 r12 = __builtin_shufflevector(r1, r2, 0, 1, 2, 3, 4, 5, 6, 7);
+        const V8 a = __builtin_bit_cast(V8, r12);
 #pragma unroll
         for (int g = 0; g < QG; ++g) o[g][tt] = mfma32x32<T>(a, pb[g][c], o[g][tt]);
       }
     }
-    if (t + 1 < t_end) sstore(buf ^ 1);
     __syncthreads();
   }
 
