@@ -39,6 +39,8 @@ def test_prefill_baseline_config(dev, window):
     (1, 64, 70, 2, 1, 64, False, (10, 3)),       # two-sided window
     (1, 40, 20, 2, 2, 128, True, (-1, -1)),      # Sq > Sk: early rows see nothing -> 0
     (2, 33, 33, 6, 2, 128, True, (-1, -1)),      # G = 3: one head per block
+    (2, 300, 300, 8, 4, 128, True, (100, 0)),    # 8 (batch, head group) pairs: XCD-grouped order
+    (1, 200, 260, 16, 8, 64, True, (-1, -1)),    # same with D=64, Sq < Sk, ragged last tile
 ])
 def test_prefill_shapes(dev, dtype, b, sq, sk, hq, hkv, d, causal, window):
     q, k, v = _qkv(b, sq, sk, hq, hkv, d, dtype, seed=1)

@@ -112,9 +112,19 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
   const int qt_len = wph * 32 * QG;
   const int nqt = (p.Sq + qt_len - 1) / qt_len;
   const int nhg = p.Hq / hpb;
-  const int bid = blockIdx.x;
-  const int qt = nqt - 1 - bid / (p.B * nhg); // heavy (late) query tiles first
-  const int rest = bid % (p.B * nhg);
+  const int npair = p.B * nhg;
+  int qt, rest;
+  if (npair % 8 == 0) {
+    // workgroups are dealt to the 8 XCDs round-robin (XCD = blockIdx % 8):
+    // each XCD gets whole (batch, head group) pairs, so the K / V tiles its
+    // blocks share stay in its own L2; heavy (late) query tiles start first
+    const int per = npair / 8, j = blockIdx.x / 8;
+    rest = (blockIdx.x % 8) * per + j % per;
+    qt = nqt - 1 - j / per;
+  } else {
+    qt = nqt - 1 - blockIdx.x / npair;
+    rest = blockIdx.x % npair;
+  }
   const int b = rest / nhg, hg = rest % nhg;
   const int hq = hg * hpb + w / wph;
   const int hk = (hg * hpb) / G;
@@ -156,26 +166,56 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
                       : zero;
   }
 
-  // K and V tiles go HBM/L2 -> LDS by LDS-DMA (no staging registers):
-  // instruction i of wave w fills 64 slots = 64/CPR keys; lane l fetches the
-  // chunk that lands in its slot. Keys past Sk are clamped to Sk-1 (finite
-  // data; those scores are masked, so their P is 0, on the edge tile).
+  // The block's waves form two groups of NW/2 (waves w and w + NW/2 share a
+  // SIMD). The leading group runs half an iteration ahead of the trailing
+  // one, so on every SIMD one wave's MFMA phase (PV of tile t-1, then QK^T of
+  // tile t) overlaps the other wave's softmax phase (VALU). Each iteration
+  // has two workgroup barriers, one per phase change; the trailing group
+  // passes one barrier before its first iteration, the leading group one
+  // after its last.
+  const bool lead = __builtin_amdgcn_readfirstlane(w) < NW / 2; // wave-uniform
+  constexpr int NWL = NW / 2;
+
+  // K and V tiles go HBM/L2 -> LDS by LDS-DMA (no staging registers), issued
+  // by one group of NW/2 waves: instruction i of the group's wave w fills 64
+  // slots = 64/CPR keys; lane l fetches the chunk that lands in its slot. The
+  // address is a wave-uniform tile base plus a per-lane 32-bit byte offset
+  // fixed for the whole loop (the launch checks 64 rows fit in 2^31 bytes).
+  // Keys past Sk are clamped to Sk-1 on the last tile (finite data; those
+  // scores are masked, so their P is 0).
   constexpr int KPI = 64 / CPR;                 // keys per DMA instruction
-  constexpr int KDMA = kKvTile / KPI / NW;      // DMA instructions per wave per tile
+  constexpr int KDMA = kKvTile / KPI / NWL;     // DMA instructions per wave per tile
+  const int wu = __builtin_amdgcn_readfirstlane(w) % NWL; // wave index within its group
   const int dkey = lane / CPR, dslot = lane % CPR;
-  auto gload = [&](int t, int buf) {
-    const int kb = t * kKvTile;
+  unsigned koff[KDMA], voff[KDMA];
 #pragma unroll
-    for (int i = 0; i < KDMA; ++i) {
-      const int key0 = (i * NW + w) * KPI; // first key of the instruction
-      const int key = key0 + dkey;
-      const int kk = min(kb + key, p.Sk - 1);
-      __builtin_amdgcn_global_load_lds(
-          (const void *)(kp + (int64_t)kk * p.k_ss + (dslot ^ (key & (CPR - 1))) * 8),
-          (__attribute__((address_space(3))) void *)&sm.k[buf][key0 * CPR], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(
-          (const void *)(vp + (int64_t)kk * p.v_ss + (dslot ^ vswz<D>(key)) * 8),
-          (__attribute__((address_space(3))) void *)&sm.v[buf][key0 * CPR], 16, 0, 0);
+  for (int i = 0; i < KDMA; ++i) {
+    const int key = (i * NWL + wu) * KPI + dkey;
+    koff[i] = (unsigned)((key * p.k_ss + (dslot ^ (key & (CPR - 1))) * 8) * (int64_t)sizeof(T));
+    voff[i] = (unsigned)((key * p.v_ss + (dslot ^ vswz<D>(key)) * 8) * (int64_t)sizeof(T));
+  }
+  // one DMA instruction (i < KDMA) of the tile starting at key t * kKvTile
+  auto tile_load = [&](const T *base, int64_t ss, unsigned off, V8 *dst, int t, int i, bool kswz) {
+    const int kb = t * kKvTile;
+    const char *tb = (const char *)(base + (int64_t)kb * ss);
+    const int key0 = (i * NWL + wu) * KPI;
+    if (kb + kKvTile > p.Sk) {
+      const int key = key0 + dkey, kk = min(key, p.Sk - 1 - kb);
+      const int ch = kswz ? (dslot ^ (key & (CPR - 1))) : (dslot ^ vswz<D>(key));
+      off = (unsigned)((kk * ss + ch * 8) * (int64_t)sizeof(T));
+    }
+    __builtin_amdgcn_global_load_lds((const void *)(tb + off),
+                                     (__attribute__((address_space(3))) void *)&dst[key0 * CPR],
+                                     16, 0, 0);
+  };
+  // DMA instruction j of an iteration: K tile tk (j < KDMA) or V tile tv;
+  // a negative tile index skips it
+  constexpr int NDMA = 2 * KDMA;
+  auto dma = [&](int j, int tk, int kbuf, int tv, int vbuf) {
+    if (j < KDMA) {
+      if (tk >= 0) tile_load(kp, p.k_ss, koff[j], sm.k[kbuf], tk, j, true);
+    } else {
+      if (tv >= 0) tile_load(vp, p.v_ss, voff[j - KDMA], sm.v[vbuf], tv, j - KDMA, false);
     }
   };
 
@@ -190,14 +230,20 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
 #pragma unroll
   for (int g = 0; g < QG; ++g) m_run[g] = -INFINITY, l_run[g] = 0.f;
 
-  if (t_begin < t_end) gload(t_begin, 0);
-  __syncthreads(); // (its fence also drains the DMA)
-  for (int t = t_begin; t < t_end; ++t) {
-    const int buf = (t - t_begin) & 1;
-    if (t + 1 < t_end) gload(t + 1, buf ^ 1);
-    const int kb = t * kKvTile;
+  f32x16 s[QG][2];
+  V8 pb[QG][4];
 
-    f32x16 s[QG][2];
+  // S^T = K Q^T for the K tile in slot buf. The K fragments of step ks + 2
+  // are requested before the MFMAs of step ks (scheduling barriers keep the
+  // compiler from pulling the reads back next to their use), so LDS latency
+  // hides behind the matrix work.
+  auto qk = [&](int buf) {
+    auto kfrag = [&](int ks, int st) {
+      const int key = st * 32 + ql, ch = ks * 2 + h;
+      return sm.k[buf][key * CPR + (ch ^ (key & (CPR - 1)))];
+    };
+    constexpr int KS = D / 16;
+    V8 kr[3][2];
 #pragma unroll
     for (int g = 0; g < QG; ++g)
 #pragma unroll
@@ -205,61 +251,103 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[g][st][r] = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const int key = st * 32 + ql, ch = ks * 2 + h;
-        const V8 a = sm.k[buf][key * CPR + (ch ^ (key & (CPR - 1)))];
+      for (int st = 0; st < 2; ++st) kr[ks][st] = kfrag(ks, st);
 #pragma unroll
-        for (int g = 0; g < QG; ++g) s[g][st] = mfma32x32<T>(a, qf[g][ks], s[g][st]);
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 2 < KS) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st) kr[(ks + 2) % 3][st] = kfrag(ks + 2, st);
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int g = 0; g < QG; ++g) s[g][st] = mfma32x32<T>(kr[ks % 3][st], qf[g][ks], s[g][st]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // Online softmax on raw scores: the running max m is kept unscaled and
-    // exp2(scale*log2e*(s - m)) is one FMA + v_exp_f32 per score (scale > 0
-    // preserves the max). Masking only on band edges.
+  };
+
+  // Online softmax on raw scores of tile t: the running max m is kept
+  // unscaled and exp2(scale*log2e*(s - m)) is one FMA + v_exp_f32 per score
+  // (scale > 0 preserves the max). Masking only on band edges.
+  // issue(j) is called at evenly spaced points of the exponentials with
+  // j = 0 .. NDMA-1 (the trailing waves put their DMA instructions there: a
+  // burst of them would stall issue on the vector-memory queue)
+  auto softmax = [&](int t, auto &&issue) {
+    const int kb = t * kKvTile;
     const bool edge = (p.right >= 0 && kb + kKvTile - 1 > q0 + off + p.right) ||
                       (p.left >= 0 && kb < q_last + off - p.left) || (kb + kKvTile > p.Sk);
     const float c2 = p.scale_log2;
-    V8 pb[QG][4];
 #pragma unroll
     for (int g = 0; g < QG; ++g) {
       const int qi = qw + g * 32 + ql;
       float mt = -INFINITY;
       if (edge) {
+        // score register (st, r) holds key kb + 4h + c, c = 32st + 8(r/4) + r%4;
+        // it is kept iff lo <= key <= hi, i.e. c - A <= U unsigned with
+        // A = lo - kb - 4h, U = hi - lo (an empty range gets A = 2^30, U = 0)
+        const int qpos = qi + off;
+        int hi = p.Sk - 1;
+        if (p.right >= 0) hi = min(hi, qpos + p.right);
+        const int lo = p.left >= 0 ? max(qpos - p.left, 0) : 0;
+        const int jb = kb + h * 4;
+        unsigned A = (unsigned)(lo - jb), U = (unsigned)(hi - lo);
+        if (hi < lo) A = 1u << 30, U = 0;
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int j = kb + st * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-            const int rel = j - (qi + off);
-            bool keep = j < p.Sk;
-            if (p.right >= 0) keep = keep && rel <= p.right;
-            if (p.left >= 0) keep = keep && rel >= -p.left;
-            s[g][st][r] = keep ? s[g][st][r] : -INFINITY;
+            const unsigned c = st * 32 + (r >> 2) * 8 + (r & 3);
+            s[g][st][r] = c - A <= U ? s[g][st][r] : -INFINITY;
           }
       }
+      // max and sum as trees: a 32-long dependent chain of VALU ops costs
+      // its full latency per step
+      float mx[8];
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+      for (int i = 0; i < 8; ++i)
+        mx[i] = fmaxf(fmaxf(s[g][0][i], s[g][0][i + 8]), fmaxf(s[g][1][i], s[g][1][i + 8]));
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[g][st][r]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-      const float m_new = fmaxf(m_run[g], mt);
+      for (int n = 4; n >= 1; n >>= 1)
+#pragma unroll
+        for (int i = 0; i < n; ++i) mx[i] = fmaxf(mx[i], mx[i + n]);
+      mt = fmaxf(mt, mx[0]);
+      {
+        // the other half of the wave holds the other 4-key groups
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt),
+                                                         false, false);
+        mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      }
+      // lazy rescale: the reference max m_run only moves when the tile max
+      // exceeds it by more than 8 in the exp2 domain (or on the first finite
+      // tile), so P <= 2^8 and O, l keep fp32 headroom; O / l is unchanged by
+      // the choice of m_run, and the O rescale then runs on few tiles
+      const bool move = (mt - m_run[g]) * c2 > 8.f; // false for NaN (both -inf)
+      const float m_new = move ? mt : m_run[g];
       const float mc = m_new == -INFINITY ? 0.f : m_new * c2;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[g] * c2 - mc);
-      float psum = 0.f;
+      const float alpha = move ? __builtin_amdgcn_exp2f(m_run[g] * c2 - mc) : 1.f;
+      float ps[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ps[i] = 0.f;
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
+          constexpr int kStride = 32 / NDMA;
+          if (g == 0 && (st * 16 + r) % kStride == 0) issue((st * 16 + r) / kStride);
           const float e = __builtin_amdgcn_exp2f(fmaf(s[g][st][r], c2, -mc));
           s[g][st][r] = e;
-          psum += e;
+          ps[r & 7] += e;
         }
-      l_run[g] = l_run[g] * alpha + psum;
+#pragma unroll
+      for (int n = 4; n >= 1; n >>= 1)
+#pragma unroll
+        for (int i = 0; i < n; ++i) ps[i] += ps[i + n];
+      l_run[g] = l_run[g] * alpha + ps[0];
       m_run[g] = m_new;
-      // the running max rarely moves after the first tiles: skip the O
-      // rescale (a multiply by exactly 1) unless some lane's max changed
-      if (__any(alpha != 1.f)) {
+      if (__any(move)) {
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
@@ -270,35 +358,90 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
 #pragma unroll
         for (int j = 0; j < 8; ++j) pb[g][c][j] = from_f32<T>(s[g][c >> 1][(c & 1) * 8 + j]);
     }
+  };
 
-    // O^T += V^T P^T: the A operand of 16-key step c for lane half h holds
-    // keys 16c + 4h + 0..3 (first read) and 16c + 8 + 4h + 0..3 (second), the
-    // key order of the score registers (P stays the B operand unchanged).
+  // O^T += V^T P^T for the V tile in slot buf: the A operand of 16-key step c
+  // for lane half h holds keys 16c + 4h + 0..3 (first read) and
+  // 16c + 8 + 4h + 0..3 (second), the key order of the score registers (P
+  // stays the B operand unchanged). The V fragments of step c + 2 are
+  // requested before the MFMAs of step c.
+  auto pv = [&](int buf) {
     typedef short s16x4 __attribute__((ext_vector_type(4)));
     typedef short s16x8 __attribute__((ext_vector_type(8)));
     const int grp = lane >> 4, a4 = lane & 3, c4 = (lane >> 2) & 3;
     const __attribute__((address_space(3))) char *vbase =
         (const __attribute__((address_space(3))) char *)&sm.v[buf][0];
+    auto vfrag = [&](int c, int tt) {
+      const int key1 = 16 * c + 4 * (grp >> 1) + c4, key2 = key1 + 8;
+      const int d0 = tt * 32 + 16 * (grp & 1) + 4 * a4; // this lane's 4 columns
+      const int o1 = key1 * D * 2 + (((d0 >> 3) ^ vswz<D>(key1)) << 4) + ((d0 & 7) << 1);
+      const int o2 = key2 * D * 2 + (((d0 >> 3) ^ vswz<D>(key2)) << 4) + ((d0 & 7) << 1);
+      const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4 *)(vbase + o1));
+      const s16x4 r2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4 *)(vbase + o2));
+      const s16x8 r12 = __builtin_shufflevector(r1, r2, 0, 1, 2, 3, 4, 5, 6, 7);
+      return __builtin_bit_cast(V8, r12);
+    };
+    V8 vr[3][NT];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) vr[c][tt] = vfrag(c, tt);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int key1 = 16 * c + 4 * (grp >> 1) + c4, key2 = key1 + 8;
+      if (c + 2 < 4) {
 #pragma unroll
-      for (int tt = 0; tt < NT; ++tt) {
-        const int d0 = tt * 32 + 16 * (grp & 1) + 4 * a4; // this lane's 4 columns
-        const int o1 = key1 * D * 2 + (((d0 >> 3) ^ vswz<D>(key1)) << 4) + ((d0 & 7) << 1);
-        const int o2 = key2 * D * 2 + (((d0 >> 3) ^ vswz<D>(key2)) << 4) + ((d0 & 7) << 1);
-        const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4 *)(vbase + o1));
-        const s16x4 r2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4 *)(vbase + o2));
-        const s16x8 r12 = __builtin_shufflevector(r1, r2, 0, 1, 2, 3, 4, 5, 6, 7);
-        const V8 a = __builtin_bit_cast(V8, r12);
-#pragma unroll
-        for (int g = 0; g < QG; ++g) o[g][tt] = mfma32x32<T>(a, pb[g][c], o[g][tt]);
+        for (int tt = 0; tt < NT; ++tt) vr[(c + 2) % 3][tt] = vfrag(c + 2, tt);
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (int g = 0; g < QG; ++g) o[g][tt] = mfma32x32<T>(vr[c % 3][tt], pb[g][c], o[g][tt]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
+  };
+
+  // Slots: K tile t and V tile t live in slot (t - t_begin) & 1. The leading
+  // group's MFMA phase of iteration t (PV of V(t-1), QK^T of K(t)) shares its
+  // interval with the trailing group's softmax phase of iteration t-1, in
+  // which the trailing waves request K(t+1) (into the slot of K(t-1)) and
+  // V(t) (into the slot of V(t-2)); both slots were last read in the
+  // trailing group's MFMA phase of iteration t-1, the interval before. They
+  // wait for them at the end of their next MFMA phase, before the barrier
+  // after which the leading group reads them. K(t_begin), K(t_begin+1) and
+  // V(t_begin) are loaded up front.
+  // barrier without the fence of __syncthreads (which would drain the DMA);
+  // the empty asm keeps the compiler from moving LDS accesses across it
+  auto bar = [] {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  if (t_begin < t_end) {
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) {
+      if (lead) dma(j, j < KDMA ? t_begin : -1, 0, -1, 0);
+      else dma(j, t_begin + 1 < t_end ? t_begin + 1 : -1, 1, t_begin, 0);
+    }
   }
+  __syncthreads(); // (its fence also drains the DMA)
+  if (!lead) bar();
+  for (int t = t_begin; t < t_end; ++t) {
+    const int buf = (t - t_begin) & 1;
+    if (t > t_begin) pv(buf ^ 1);
+    qk(buf);
+    if (!lead) __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): K(t+1), V(t) landed
+    bar();
+    const int tk = t + 2 < t_end ? t + 2 : -1, tv = t + 1 < t_end ? t + 1 : -1;
+    softmax(t, [&](int j) {
+      if (!lead) dma(j, tk, buf, tv, buf ^ 1);
+    });
+    bar();
+  }
+  if (t_begin < t_end) pv((t_end - 1 - t_begin) & 1);
+  if (lead) bar();
 
   typedef typename VecT<T>::v4 V4;
 #pragma unroll
@@ -695,7 +838,10 @@ template <typename T>
 static int launch_prefill(const AttnArgs &a, int64_t D, hipStream_t st, const char *name) {
   if (a.B == 0 || a.Sq == 0) return TPP_OK;
   const int G = a.Hq / a.Hkv;
-  if ((D == 64 || D == 128) && strides16(a)) {
+  // the tiled kernel addresses a 64-row K / V tile with 32-bit byte offsets
+  const bool rows_fit = a.k_ss >= 0 && a.v_ss >= 0 && (int64_t)kKvTile * a.k_ss * 2 < (1LL << 31) &&
+                        (int64_t)kKvTile * a.v_ss * 2 < (1LL << 31);
+  if ((D == 64 || D == 128) && strides16(a) && rows_fit) {
     const int hpb = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
     constexpr int QG = kPrefillQG;
     constexpr int NW = kPrefillWaves;
