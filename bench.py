@@ -110,7 +110,7 @@ def measure_kernels(model, dec, cfg, L):
 
     us = event_time_us(attn, nl)
     attn_bytes = 2 * B * Hkv * L * D * 2 + 2 * B * H * D * 2
-    out.append(hbm_entry("attn_decode_kernel (+combine) B8 16/8 d128 L%d" % L, us, attn_bytes))
+    out.append(hbm_entry("attn_decode_kernel (splits merged in-kernel) B8 16/8 d128 L%d" % L, us, attn_bytes))
     attn_us = us
 
     def gemv_entry(name, wget, n, k, xin, fn=None):
@@ -282,7 +282,7 @@ def measure_configs():
     seq = torch.full((B,), L, dtype=torch.int32, device=dev)
     o = torch.empty_like(q)
     t = event_time_us(lambda: C.attn_decode(q, kc, vc, seq, 0.0, -1, o), 8)
-    out.append(_cfg_entry(3, "attn_decode B32 16/8 d128 L4096 (+merge)", "hbm", t, t,
+    out.append(_cfg_entry(3, "attn_decode B32 16/8 d128 L4096", "hbm", t, t,
                           2 * B * Hkv * L * D * 2 + 2 * B * Hq * D * 2))
     del kc, vc
     return out
@@ -553,7 +553,7 @@ def main():
                                "head_dim 128, SwiGLU 3072, vocab 151936), batch 8, prefill 2048",
                    "global_batch": BATCH, "prefill_len": PREFILL, "decode_steps": K,
                    "parallelism": "single GPU"},
-        "roofline": {"kernel": "attn_decode_kernel + attn_decode_merge_kernel", "bound": "hbm",
+        "roofline": {"kernel": "attn_decode_kernel", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(L),
                      "bytes_per_launch": attn_bytes, "avg_launch_us": round(attn_us, 3),

@@ -213,8 +213,11 @@ int tpp_attn_prefill(const void *q, const void *k, const void *v, void *o,
                      int window_left, int window_right, int dtype,
                      void *stream);
 
-/* Bytes of workspace tpp_attn_decode needs (no initialisation required;
- * calls that share a workspace must be ordered, e.g. on one stream). */
+/* Bytes of workspace tpp_attn_decode needs. The workspace must be 128-byte
+ * aligned and its first 64 KiB zero-filled before the first use: they hold
+ * per-(batch, KV head) arrival counters that every call leaves at zero
+ * again (calls of any shape may share the workspace, but nothing else may
+ * write those bytes). Calls that share it must be ordered (e.g. one stream). */
 size_t tpp_attn_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv,
                                       int64_t D, int64_t Lmax);
 

@@ -103,6 +103,27 @@ def test_decode_ragged_lengths(dev, hq, hkv, d):
     close(o, oracle.decode_attention(q, kc, vc, lens.tolist()), what="ragged decode")
 
 
+def test_decode_shared_workspace_across_shapes(dev):
+    """Decode calls of different shapes share one workspace (its arrival
+    counters must be back at zero after every call, and no call's partials may
+    land on them, whether it merges in-kernel (pairs a multiple of 8) or with
+    the merge kernel (5 x 4 pairs)): alternate four shapes twice, each
+    against the oracle."""
+    g = torch.Generator().manual_seed(11)
+    cases = []
+    for B, hq, hkv, d, Lmax in [(4, 16, 8, 128, 600), (5, 8, 4, 128, 300), (8, 16, 8, 64, 200),
+                                (2, 8, 4, 128, 900)]:
+        q = torch.randn(B, 1, hq, d, generator=g).bfloat16()
+        kc = torch.randn(B, hkv, Lmax, d, generator=g).bfloat16()
+        vc = torch.randn(B, hkv, Lmax, d, generator=g).bfloat16()
+        lens = torch.randint(1, Lmax + 1, (B,), generator=g, dtype=torch.int32)
+        cases.append((q, kc, vc, lens, oracle.decode_attention(q, kc, vc, lens.tolist())))
+    dcases = [(q.to(dev), kc.to(dev), vc.to(dev), lens.to(dev), e) for q, kc, vc, lens, e in cases]
+    for rep in range(2):
+        for i, (q, kc, vc, lens, e) in enumerate(dcases):
+            close(decode_attention(q, kc, vc, lens), e, what=f"decode shape {i} pass {rep}")
+
+
 def test_decode_window_and_matches_prefill_path(dev):
     g = torch.Generator().manual_seed(8)
     B, Hq, Hkv, D, L = 3, 4, 2, 128, 300

@@ -526,6 +526,11 @@ constexpr int kDecMaxG = 8;
 constexpr int kDecU = 4; // key passes per load batch (two batches in flight)
 
 constexpr int kDecMaxSplit = 256;
+#ifndef TPP_DEC_INLINE_MERGE
+#define TPP_DEC_INLINE_MERGE 1
+#endif
+constexpr bool kDecInlineMerge = TPP_DEC_INLINE_MERGE;
+constexpr int64_t kDecCounterBytes = 65536; // arrival counters region of the workspace
 
 // RMSNorm (optional) + rotate-half RoPE of one head row held as 8 values per
 // lane by LPK lanes (lane dp owns d = 8 dp .. 8 dp + 7), rounded to T at the
@@ -560,7 +565,8 @@ template <typename T, int D, int G, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const int *__restrict__ seqlens,
                                                               int fixed_len, float *__restrict__ ws_o,
                                                               float *__restrict__ ws_ml, int chunk,
-                                                              int nsplit, DecodeFuse fz) {
+                                                              int nsplit, DecodeFuse fz,
+                                                              int *__restrict__ counters) {
   typedef typename VecT<T>::v8 V8;
   constexpr int LPK = D / 8;        // lanes per key
   constexpr int KPW = kWave / LPK;  // keys per wave pass
@@ -570,7 +576,17 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
 
   const int lane = lane_id(), w = wave_id();
   const int row = lane / LPK, dp = lane % LPK;
-  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  if (counters) {
+    // one-dimensional grid; workgroups are dealt to the 8 XCDs round-robin
+    // (XCD = blockIdx % 8): all splits of a (batch, KV head) pair share an
+    // XCD, so their partials meet in that XCD's L2
+    const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+    const int pair = (slot / nsplit) * 8 + xcd;
+    split = slot % nsplit;
+    hk = pair % p.Hkv;
+    b = pair / p.Hkv;
+  }
   const int Lraw = seqlens ? seqlens[b] : fixed_len;
   const int L = Lraw < p.Sk ? (Lraw > 0 ? Lraw : 0) : p.Sk; // never read past the cache
   int lo = 0;
@@ -756,11 +772,54 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
       continue;
     }
     const int64_t slot = ((int64_t)b * p.Hq + hq) * nsplit + split;
-    ws_o[slot * D + d] = os;
-    if (d == 0) {
-      ws_ml[slot * 2] = mx;
-      ws_ml[slot * 2 + 1] = ls;
+    if (counters) {
+      // slot = D partial outputs, m, l, padding: whole 128-byte lines
+      float *sl = ws_o + slot * (D + 32);
+      sl[d] = os;
+      if (d == 0) sl[D] = mx, sl[D + 1] = ls;
+    } else {
+      ws_o[slot * D + d] = os;
+      if (d == 0) ws_ml[slot * 2] = mx, ws_ml[slot * 2 + 1] = ls;
     }
+  }
+  if (!counters || nsplit == 1) return;
+  // The last block of the pair to finish merges the splits. Every thread
+  // waits for its partial stores to reach L2 (an explicit vmcnt(0): the
+  // workgroup-scope fence of __syncthreads does not wait for global stores),
+  // then one thread counts the block in with an atomic in L2; the block that
+  // takes the count to nsplit reads the other partials from the same L2.
+  // Each partial slot is whole 128-byte lines written by one block only, and
+  // a block reads other blocks' slots only here, so this CU's L1 (clean at
+  // kernel start) holds no stale copy of them.
+  __shared__ int s_last;
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
+  __syncthreads();
+  const int pair = b * p.Hkv + hk;
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(&counters[pair], 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    s_last = old == nsplit - 1;
+    if (old == nsplit - 1) // leave the counter at 0 for the next launch
+      __hip_atomic_store(&counters[pair], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int gi = idx / D, d = idx % D;
+    const float *sl = ws_o + (((int64_t)b * p.Hq + hk * G + gi) * nsplit) * (D + 32);
+    float mx = -INFINITY;
+    for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, sl[sp * (D + 32) + D]);
+    const float mu = mx == -INFINITY ? 0.f : mx;
+    float ls = 0.f, os = 0.f;
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const float *q = sl + sp * (D + 32);
+      const float wgt = exp2f(q[D] - mu);
+      ls += wgt * q[D + 1];
+      os += wgt * q[d];
+    }
+    T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)(hk * G + gi) * p.o_sh;
+    op[d] = from_f32<T>(ls > 0.f ? os / ls : 0.f);
   }
 }
 
@@ -863,7 +922,8 @@ static int launch_prefill(const AttnArgs &a, int64_t D, hipStream_t st, const ch
 
 struct DecodePlan {
   int chunk, nsplit, nw;
-  size_t ws_bytes;
+  bool inline_merge; // the last split block merges (no merge kernel)
+  size_t o_bytes, ml_bytes, ws_bytes;
 };
 
 // Split-KV plan: about one 8-wave block per CU, each (batch, KV head) pair's
@@ -883,52 +943,71 @@ static DecodePlan plan_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
   pl.chunk = (int)chunk;
   pl.nsplit = (int)((Lmax + chunk - 1) / chunk);
   if (pl.nsplit < 1) pl.nsplit = 1;
-  pl.ws_bytes = pl.nsplit > 1 ? (size_t)(B * Hq * pl.nsplit) * (size_t)(D + 2) * sizeof(float) : 16;
+  pl.inline_merge = pl.nsplit > 1 && pairs % 8 == 0 && pairs * (int64_t)sizeof(int) <= kDecCounterBytes &&
+                    kDecInlineMerge;
+  const size_t slots = (size_t)(B * Hq * pl.nsplit);
+  if (pl.nsplit == 1) {
+    pl.o_bytes = pl.ml_bytes = 0;
+    pl.ws_bytes = 16;
+  } else if (pl.inline_merge) {
+    // one arrival counter per (batch, KV head) pair in a fixed region at the
+    // start (calls of every shape and mode keep partials out of it), then
+    // slots of D partial outputs + m + l padded to whole 128-byte lines
+    pl.o_bytes = slots * (size_t)(D + 32) * sizeof(float);
+    pl.ml_bytes = 0;
+    pl.ws_bytes = kDecCounterBytes + pl.o_bytes;
+  } else {
+    // the counter region stays reserved (and untouched) here too, so a
+    // workspace shared with inline-merge calls keeps its counters at zero
+    pl.o_bytes = slots * (size_t)D * sizeof(float);
+    pl.ml_bytes = slots * 2 * sizeof(float);
+    pl.ws_bytes = kDecCounterBytes + pl.o_bytes + pl.ml_bytes;
+  }
   return pl;
 }
 
 template <typename T, int D, int G>
 static void launch_decode_g(const AttnArgs &a, dim3 grid, const int *seqlens, int L, float *ws_o,
-                            float *ws_ml, const DecodePlan &pl, const DecodeFuse &fz,
+                            float *ws_ml, int *counters, const DecodePlan &pl, const DecodeFuse &fz,
                             hipStream_t st) {
   if constexpr (G <= 2) {
     if (pl.nw == 8) {
       attn_decode_kernel<T, D, G, 8><<<grid, dim3(512), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
-                                                                 pl.chunk, pl.nsplit, fz);
+                                                                 pl.chunk, pl.nsplit, fz, counters);
     } else {
       attn_decode_kernel<T, D, G, 4><<<grid, dim3(256), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
-                                                                 pl.chunk, pl.nsplit, fz);
+                                                                 pl.chunk, pl.nsplit, fz, counters);
     }
   } else
     attn_decode_kernel<T, D, G, 4><<<grid, dim3(256), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
-                                                               pl.chunk, pl.nsplit, fz);
-  if (pl.nsplit > 1)
-    attn_decode_merge_kernel<T, D, G><<<dim3(grid.y, grid.z), dim3(G * D), 0, st>>>(
+                                                               pl.chunk, pl.nsplit, fz, counters);
+  if (pl.nsplit > 1 && !counters)
+    attn_decode_merge_kernel<T, D, G><<<dim3(a.Hkv, a.B), dim3(G * D), 0, st>>>(
         a, ws_o, ws_ml, pl.nsplit);
 }
 
 template <typename T, int D>
 static void launch_decode_d(const AttnArgs &a, int G, dim3 grid, const int *seqlens, int L,
-                            float *ws_o, float *ws_ml, const DecodePlan &pl, const DecodeFuse &fz,
-                            hipStream_t st) {
+                            float *ws_o, float *ws_ml, int *counters, const DecodePlan &pl,
+                            const DecodeFuse &fz, hipStream_t st) {
   switch (G) {
-  case 1: launch_decode_g<T, D, 1>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
-  case 2: launch_decode_g<T, D, 2>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
-  case 3: launch_decode_g<T, D, 3>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
-  case 4: launch_decode_g<T, D, 4>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
-  case 5: launch_decode_g<T, D, 5>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
-  case 6: launch_decode_g<T, D, 6>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
-  case 7: launch_decode_g<T, D, 7>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
-  default: launch_decode_g<T, D, 8>(a, grid, seqlens, L, ws_o, ws_ml, pl, fz, st); break;
+  case 1: launch_decode_g<T, D, 1>(a, grid, seqlens, L, ws_o, ws_ml, counters, pl, fz, st); break;
+  case 2: launch_decode_g<T, D, 2>(a, grid, seqlens, L, ws_o, ws_ml, counters, pl, fz, st); break;
+  case 3: launch_decode_g<T, D, 3>(a, grid, seqlens, L, ws_o, ws_ml, counters, pl, fz, st); break;
+  case 4: launch_decode_g<T, D, 4>(a, grid, seqlens, L, ws_o, ws_ml, counters, pl, fz, st); break;
+  case 5: launch_decode_g<T, D, 5>(a, grid, seqlens, L, ws_o, ws_ml, counters, pl, fz, st); break;
+  case 6: launch_decode_g<T, D, 6>(a, grid, seqlens, L, ws_o, ws_ml, counters, pl, fz, st); break;
+  case 7: launch_decode_g<T, D, 7>(a, grid, seqlens, L, ws_o, ws_ml, counters, pl, fz, st); break;
+  default: launch_decode_g<T, D, 8>(a, grid, seqlens, L, ws_o, ws_ml, counters, pl, fz, st); break;
   }
 }
 
 template <typename T>
 static void launch_decode(const AttnArgs &a, int64_t D, int G, dim3 grid, const int *seqlens,
-                          int L, float *ws_o, float *ws_ml, const DecodePlan &pl,
+                          int L, float *ws_o, float *ws_ml, int *counters, const DecodePlan &pl,
                           const DecodeFuse &fz, hipStream_t st) {
-  if (D == 128) launch_decode_d<T, 128>(a, G, grid, seqlens, L, ws_o, ws_ml, pl, fz, st);
-  else launch_decode_d<T, 64>(a, G, grid, seqlens, L, ws_o, ws_ml, pl, fz, st);
+  if (D == 128) launch_decode_d<T, 128>(a, G, grid, seqlens, L, ws_o, ws_ml, counters, pl, fz, st);
+  else launch_decode_d<T, 64>(a, G, grid, seqlens, L, ws_o, ws_ml, counters, pl, fz, st);
 }
 
 } // namespace tpp
@@ -993,14 +1072,19 @@ static int decode_impl(const char *name, AttnArgs &a, int64_t D, int64_t Lmax,
                      kDecMaxG);
   if (!strides16(a)) return set_error(TPP_E_INVALID, "%s: 16-byte alignment required", name);
   const DecodePlan pl = plan_decode(a.B, a.Hq, a.Hkv, D, Lmax);
-  if (!workspace || ws_bytes < pl.ws_bytes || !aligned16(workspace))
-    return set_error(TPP_E_WORKSPACE, "%s: workspace of %zu bytes required", name, pl.ws_bytes);
-  float *ws_o = (float *)workspace;
-  float *ws_ml = ws_o + (size_t)((int64_t)a.B * a.Hq * pl.nsplit) * D;
+  if (!workspace || ws_bytes < pl.ws_bytes || (uintptr_t)workspace % 128 != 0)
+    return set_error(TPP_E_WORKSPACE, "%s: 128-byte aligned workspace of %zu bytes required",
+                     name, pl.ws_bytes);
+  int *counters = pl.inline_merge ? (int *)workspace : nullptr;
+  float *ws_o = (float *)((char *)workspace + kDecCounterBytes);
+  float *ws_ml = (float *)((char *)ws_o + pl.o_bytes);
   hipStream_t st = as_stream(stream);
-  const dim3 grid((unsigned)pl.nsplit, (unsigned)a.Hkv, (unsigned)a.B);
+  const dim3 grid = pl.inline_merge
+                        ? dim3((unsigned)(pl.nsplit * a.Hkv * a.B))
+                        : dim3((unsigned)pl.nsplit, (unsigned)a.Hkv, (unsigned)a.B);
   return TPP_DISPATCH_HALF(dtype, [&] {
-    launch_decode<T>(a, D, a.Hq / a.Hkv, grid, seqlens, (int)Lmax, ws_o, ws_ml, pl, fz, st);
+    launch_decode<T>(a, D, a.Hq / a.Hkv, grid, seqlens, (int)Lmax, ws_o, ws_ml, counters, pl, fz,
+                     st);
     return check_launch(name);
   });
 }

@@ -432,11 +432,15 @@ std::vector<at::Tensor> gemv_argmax(at::Tensor input, at::Tensor weight,
 // Per-device workspace for tpp_attn_decode, allocated once and reused, so a
 // captured decode graph keeps one stable pointer. Intentionally leaked: no
 // tensor destructor runs after the caching allocator is torn down at exit.
-at::Tensor cached_workspace(const at::Tensor &like, size_t bytes) {
-  static std::vector<at::Tensor> *cache = new std::vector<at::Tensor>(64);
+// Zero-filled per-device scratch reused across calls on one stream. Slot 1
+// belongs to decode attention alone: its arrival counters must stay zero
+// between calls, which the kernel guarantees but another user of the same
+// bytes would not.
+at::Tensor cached_workspace(const at::Tensor &like, size_t bytes, int slot = 0) {
+  static std::vector<at::Tensor> *cache = new std::vector<at::Tensor>(128);
   const int dev = like.device().index();
   TORCH_CHECK(dev >= 0 && dev < 64, "device index out of range");
-  at::Tensor &ws = (*cache)[dev];
+  at::Tensor &ws = (*cache)[dev * 2 + slot];
   if (!ws.defined() || (size_t)ws.numel() * 4 < bytes) {
     int64_t n = (int64_t)((bytes + 3) / 4);
     n = n < (1 << 20) ? (1 << 20) : n;
@@ -547,7 +551,7 @@ at::Tensor attn_decode(at::Tensor q, at::Tensor k_cache, at::Tensor v_cache,
     o = torch::empty_like(q);
   }
   const size_t wsb = tpp_attn_decode_workspace_size(B, Hq, Hkv, D, Lmax);
-  at::Tensor ws = cached_workspace(q, wsb);
+  at::Tensor ws = cached_workspace(q, wsb, 1);
   const int64_t qs[3] = {q.stride(0), q.stride(1), q.stride(2)};
   const int64_t ks[3] = {k_cache.stride(0), k_cache.stride(2), k_cache.stride(1)};
   const int64_t vs[3] = {v_cache.stride(0), v_cache.stride(2), v_cache.stride(1)};
@@ -603,7 +607,7 @@ at::Tensor attn_decode_fused(at::Tensor qkv, c10::optional<at::Tensor> q_norm_w,
   c10::DeviceGuard g(qkv.device());
   auto o = torch::empty({B, 1, Hq, D}, qkv.options());
   const size_t wsb = tpp_attn_decode_workspace_size(B, Hq, Hkv, D, Lmax);
-  at::Tensor ws = cached_workspace(qkv, wsb);
+  at::Tensor ws = cached_workspace(qkv, wsb, 1);
   const int64_t ks[3] = {k_cache.stride(0), k_cache.stride(2), k_cache.stride(1)};
   const int64_t vs[3] = {v_cache.stride(0), v_cache.stride(2), v_cache.stride(1)};
   const int64_t os[3] = {o.stride(0), o.stride(1), o.stride(2)};
