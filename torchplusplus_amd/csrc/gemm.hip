@@ -40,7 +40,17 @@ __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 
 // K-tile depth and ring stages of the 256x256 tile (64 KB per stage at BK 64;
 // a 4-stage ring of BK 32 tiles measured no faster)
-constexpr int kBigBK = 64, kBigNST = 2;
+#ifndef TPP_BIG_BK
+#define TPP_BIG_BK 64
+#define TPP_BIG_NST 2
+#endif
+#ifndef TPP_SMALL_BK
+#define TPP_SMALL_BK 64
+#define TPP_SMALL_NST 2
+#endif
+constexpr int kBigBK = TPP_BIG_BK, kBigNST = TPP_BIG_NST;
+// the same for the 128-row tiles (4 waves)
+constexpr int kSmallBK = TPP_SMALL_BK, kSmallNST = TPP_SMALL_NST;
 // below this many outputs the register-staged kernel's smaller LDS footprint
 // (several blocks per CU) wins over the deeper DMA ring
 constexpr int64_t kDmaMinMN = 256 * 128 * 128;
@@ -409,7 +419,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
 // 64-column pairs per wave (FN even).
 static int pick_dma_tile(int64_t M, int64_t N, bool swiglu, int cus) {
   struct Cand { int bm, bn, fn_wave; double eff; };
-  // 128x128 / 128x192 / 128x256: 4 waves (2x2); 256x256: 8 waves (4x2) of 64x128
+  // 128x128 / 128x192 / 128x256: 8 waves (4x2) of 32x64 / 32x96 / 32x128, so
+  // two waves share each SIMD even at one block per CU (measured 7% faster
+  // than 4 waves of 64-row strips at the BASELINE Linear+act shape);
+  // 256x256: 8 waves (4x2) of 64x128
   const Cand cands[] = {{128, 128, 2, 0.95}, {128, 192, 3, 1.0}, {128, 256, 4, 1.0},
                         {256, 256, 4, 1.25}};
   int best = -1;
@@ -488,9 +501,9 @@ static int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, v
     if ((M + 127) / 128 * ((N + 127) / 128) > 0x7fffffffLL)
       return set_error(TPP_E_UNSUPPORTED, "%s: too many tiles", name);
     switch (pick_dma_tile(M, N, EPI == kGSwiGLU, device_cus())) {
-    case 0: launch_dma<T, EPI, ACT, 2, 2, 2, 2, 64, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    case 1: launch_dma<T, EPI, ACT, 2, 3, 2, 2, 64, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    case 2: launch_dma<T, EPI, ACT, 2, 4, 2, 2, 64, 2>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 0: launch_dma<T, EPI, ACT, 1, 2, 4, 2, kSmallBK, kSmallNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 1: launch_dma<T, EPI, ACT, 1, 3, 4, 2, kSmallBK, kSmallNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 2: launch_dma<T, EPI, ACT, 1, 4, 4, 2, kSmallBK, kSmallNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
     default: launch_dma<T, EPI, ACT, 2, 4, 4, 2, kBigBK, kBigNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
     }
   } else if (vec) {
