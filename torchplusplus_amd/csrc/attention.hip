@@ -531,6 +531,14 @@ constexpr int kDecMaxSplit = 256;
 #endif
 constexpr bool kDecInlineMerge = TPP_DEC_INLINE_MERGE;
 constexpr int64_t kDecCounterBytes = 65536; // arrival counters region of the workspace
+#ifndef TPP_DEC_WAVES
+#define TPP_DEC_WAVES 2048
+#endif
+constexpr int kDecWaves = TPP_DEC_WAVES; // split-KV target: waves per decode launch
+#ifndef TPP_DEC_BIG_NW
+#define TPP_DEC_BIG_NW 8
+#endif
+constexpr int kDecBigNW = TPP_DEC_BIG_NW; // waves per block when G <= 2
 
 // RMSNorm (optional) + rotate-half RoPE of one head row held as 8 values per
 // lane by LPK lanes (lane dp owns d = 8 dp .. 8 dp + 7), rounded to T at the
@@ -932,10 +940,10 @@ static DecodePlan plan_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
   DecodePlan pl{};
   const int64_t kpw = kWave / (D / 8);
   const int64_t pairs = B * Hkv > 0 ? B * Hkv : 1;
-  pl.nw = (Hkv > 0 && Hq / Hkv <= 2) ? 8 : 4; // more query heads per KV head: more VGPRs
+  pl.nw = (Hkv > 0 && Hq / Hkv <= 2) ? kDecBigNW : 4; // more query heads per KV head: more VGPRs
   const int64_t batch = pl.nw * kpw * kDecU; // keys per block-wide load batch
-  // about 2048 waves (8 per CU), in whole load batches
-  int64_t want = (2048 / pl.nw + pairs - 1) / pairs;
+  // about kDecWaves waves, in whole load batches
+  int64_t want = (kDecWaves / pl.nw + pairs - 1) / pairs;
   int64_t chunk = (Lmax + want - 1) / want;
   chunk = ((chunk + batch - 1) / batch) * batch;
   if (chunk < batch) chunk = batch;
@@ -971,8 +979,8 @@ static void launch_decode_g(const AttnArgs &a, dim3 grid, const int *seqlens, in
                             float *ws_ml, int *counters, const DecodePlan &pl, const DecodeFuse &fz,
                             hipStream_t st) {
   if constexpr (G <= 2) {
-    if (pl.nw == 8) {
-      attn_decode_kernel<T, D, G, 8><<<grid, dim3(512), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
+    if (pl.nw == kDecBigNW) {
+      attn_decode_kernel<T, D, G, kDecBigNW><<<grid, dim3(64 * kDecBigNW), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
                                                                  pl.chunk, pl.nsplit, fz, counters);
     } else {
       attn_decode_kernel<T, D, G, 4><<<grid, dim3(256), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
