@@ -149,14 +149,62 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       }
     }
   };
-  // one K batch per wave: x stays resident. With the fused RMSNorm the
-  // weights of the block's first tile are requested before the input
-  // prologue (row statistics, barrier, x loads), so the two latency chains
-  // overlap; without it x is requested first.
+  // One K batch per wave (x stays resident): the tile's weights go HBM ->
+  // LDS by LDS-DMA into this wave's slot (16 rows x 512 bytes per row set;
+  // instruction j covers rows 2j, 2j+1 with whole 128-byte lines, lane i
+  // fetching unit (i % 32) ^ row so that the MFMA-layout reads below hit 16
+  // distinct bank groups), then are read back as B operands. Loaded straight
+  // into the MFMA layout (16 rows x 64 bytes per instruction) the same
+  // weights stream at about a quarter of the rate per CU. Rows past N read
+  // row N-1 and units past K read the last unit (finite data, multiplied by
+  // x = 0 or discarded). With the fused RMSNorm the first tile's DMA is
+  // issued before the input prologue, so the two latency chains overlap.
+  constexpr int NSET = EPI == kEpiSwiGLU ? 2 : 1;
+  extern __shared__ __attribute__((aligned(16))) char gemv_smem[];
+  V8 *wslot = reinterpret_cast<V8 *>(gemv_smem) + (size_t)w * NSET * (16 * 32);
+  const int drow = lane >> 5, dpos = lane & 31;
+  auto issue_w = [&](int64_t tile, float (&res)[4]) {
+    int64_t row0, row1;
+    rows_of(tile, row0, row1);
+#pragma unroll
+    for (int set = 0; set < NSET; ++set) {
+      const int64_t rb = set == 0 ? row0 : row1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int row = 2 * j + drow;
+        const int64_t gr = rb + row < N ? rb + row : N - 1;
+        int64_t kk = k_begin + (int64_t)((dpos ^ row) * 8);
+        kk = kk < K - 8 ? kk : K - 8;
+        __builtin_amdgcn_global_load_lds(
+            (const void *)(W + gr * K + kk),
+            (__attribute__((address_space(3))) void *)(wslot + set * (16 * 32) + j * 64), 16, 0, 0);
+      }
+    }
+    if constexpr (EPI == kEpiResidual) {
+      if (w == 0 && row0 + r < N) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int b = 4 * g + i;
+          if (b < a.NB) res[i] = to_f32(((const T *)a.residual)[(int64_t)b * a.ldy + row0 + r]);
+        }
+      }
+    }
+  };
+  // the slot's weights as B operands (waits for this wave's DMA; the slot
+  // may be refilled once this returns)
+  auto fetch_w = [&](V8 (&b0)[NS], V8 (&b1)[NS]) {
+    __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8)); // vmcnt(0)
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      b0[u] = wslot[r * 32 + ((u * 4 + g) ^ r)];
+      if constexpr (EPI == kEpiSwiGLU) b1[u] = wslot[16 * 32 + r * 32 + ((u * 4 + g) ^ r)];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): reads done
+  };
   const bool x_res = k_end - k_begin <= kGemvWaveK;
-  V8 pa0[NS], pa1[NS], pb0[NS], pb1[NS];
-  float ra[4] = {0.f, 0.f, 0.f, 0.f}, rb[4] = {0.f, 0.f, 0.f, 0.f};
-  if (NORM && x_res && blockIdx.x < tiles) load_w(blockIdx.x, k_begin, pa0, pa1, ra);
+  V8 pa0[NS], pa1[NS];
+  float ra[4] = {0.f, 0.f, 0.f, 0.f};
+  if (NORM && x_res && blockIdx.x < tiles) issue_w(blockIdx.x, ra);
 
   // this wave's slice of the (normalised) input, reused by every tile
   // kept resident when the wave's K slice is one load batch (K <= 4096 for
@@ -231,7 +279,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
     }
   } else if (x_res) {
     load_x(k_begin, xa);
-    if (blockIdx.x < tiles) load_w(blockIdx.x, k_begin, pa0, pa1, ra);
+    if (blockIdx.x < tiles) issue_w(blockIdx.x, ra);
   }
 
   // per-block running argmax over all tiles (wave 0, lanes r == 0 hold it)
@@ -303,19 +351,15 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
 
   const int64_t stride = gridDim.x;
   if (x_res) {
-    // one K batch per wave: keep two tiles in flight (W of tile t + stride is
-    // requested before tile t is reduced and written)
-    for (int64_t t = blockIdx.x; t < tiles; t += 2 * stride) {
-      const int64_t t2 = t + stride;
-      if (t2 < tiles) load_w(t2, k_begin, pb0, pb1, rb);
+    // two tiles in flight: tile t in registers while the DMA of tile
+    // t + stride fills the slot
+    for (int64_t t = blockIdx.x; t < tiles; t += stride) {
+      fetch_w(pa0, pa1);
+      float rc[4] = {ra[0], ra[1], ra[2], ra[3]};
+      if (t + stride < tiles) issue_w(t + stride, ra);
       f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
       mfma_batch(xa, pa0, pa1, c0, c1);
-      finish(t, c0, c1, ra);
-      if (t2 >= tiles) break;
-      if (t2 + stride < tiles) load_w(t2 + stride, k_begin, pa0, pa1, ra);
-      f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-      mfma_batch(xa, pb0, pb1, d0, d1);
-      finish(t2, d0, d1, rb);
+      finish(t, c0, c1, rc);
     }
   } else {
     for (int64_t tile = blockIdx.x; tile < tiles; tile += stride) {
@@ -645,8 +689,11 @@ static int launch_gemv(GemvArgs a, hipStream_t st, const char *name) {
   const int64_t per = (a.K + nw - 1) / nw;
   a.kslice = (int)(((per + 31) / 32) * 32);
   const int64_t blocks = tiles < kGemvMaxBlocks ? tiles : kGemvMaxBlocks;
+  // LDS weight slots of the one-batch-per-wave path (16 rows x 512 bytes per
+  // row set and wave)
+  const size_t lds = (size_t)nw * (EPI == kEpiSwiGLU ? 2 : 1) * 16 * 512;
   gemv16_kernel<T, EPI, ACT, NORM, MAXW>
-      <<<dim3((unsigned)blocks), dim3((unsigned)(nw * 64)), 0, st>>>(a, tiles);
+      <<<dim3((unsigned)blocks), dim3((unsigned)(nw * 64)), lds, st>>>(a, tiles);
   return check_launch(name);
 }
 
