@@ -39,17 +39,18 @@ constexpr int kBM = 128, kBN = 128, kBK = 64;
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 
 // K-tile depth and ring stages of the 256x256 tile (64 KB per stage at BK 64;
-// a 4-stage ring of BK 32 tiles measured no faster)
+// 4- and 5-stage rings of BK 32 tiles measured slower)
 #ifndef TPP_BIG_BK
 #define TPP_BIG_BK 64
 #define TPP_BIG_NST 2
 #endif
 #ifndef TPP_SMALL_BK
 #define TPP_SMALL_BK 64
-#define TPP_SMALL_NST 2
+#define TPP_SMALL_NST 3
 #endif
 constexpr int kBigBK = TPP_BIG_BK, kBigNST = TPP_BIG_NST;
-// the same for the 128-row tiles (4 waves)
+// the same for the 128-row tiles (3 stages: 6% faster than 2 at the
+// Linear+act shape, 96-144 KB, one block per CU)
 constexpr int kSmallBK = TPP_SMALL_BK, kSmallNST = TPP_SMALL_NST;
 // below this many outputs the register-staged kernel's smaller LDS footprint
 // (several blocks per CU) wins over the deeper DMA ring
@@ -265,6 +266,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
                                        (__attribute__((address_space(3))) void *)(sb + (j * NWV + w) * 64),
                                        16, 0, 0);
   };
+  // DMA instruction q (0 .. NA + NB - 1) of tile kt into a stage
+  auto issue_one = [&](int stage, int kt, int q) {
+    V8 *sa = smem + stage * STG, *sb = sa + BM * CPR;
+    const int64_t ko = (int64_t)kt * BK + lkc * 8;
+    if (q < NA)
+      __builtin_amdgcn_global_load_lds((const void *)(A + (int64_t)min(arow + RPI * NWV * q, M - 1) * lda + ko),
+                                       (__attribute__((address_space(3))) void *)(sa + (q * NWV + w) * 64),
+                                       16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds((const void *)(B + (int64_t)min(brow + RPI * NWV * (q - NA), N - 1) * ldb + ko),
+                                       (__attribute__((address_space(3))) void *)(sb + ((q - NA) * NWV + w) * 64),
+                                       16, 0, 0);
+  };
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -316,26 +330,48 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
     }
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
-    if (kt + NST - 1 < nk) issue((kt + NST - 1) % NST, kt + NST - 1);
     const V8 *sa = smem + (kt % NST) * STG, *sb = sa + BM * CPR;
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
+    // operand fragments of K sub-step ks into register set ks & 1: the reads
+    // of sub-step ks + 1 are in flight while the MFMAs of ks run
+    V8 af[2][FM], bfr[2][FN];
+    auto frag = [&](int ks) {
       const int kc = ks * 2 + (lane >> 5);
-      V8 af[FM], bfr[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int row = wm * FM * 32 + i * 32 + (lane & 31);
-        af[i] = sa[row * CPR + (kc ^ swzk<BK>(row))];
+        af[ks & 1][i] = sa[row * CPR + (kc ^ swzk<BK>(row))];
       }
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int col = wn * FN * 32 + j * 32 + (lane & 31);
-        bfr[j] = sb[col * CPR + (kc ^ swzk<BK>(col))];
+        bfr[ks & 1][j] = sb[col * CPR + (kc ^ swzk<BK>(col))];
       }
+    };
+    frag(0);
+    // the next tile's DMA (into a stage every wave finished reading before
+    // the barrier) is spread between the MFMAs of the first three quarters
+    // of the step, so no wave stalls on a burst of DMA issue while the MFMA
+    // pipe waits
+    const int kn = kt + NST - 1;
+    const bool more = kn < nk;
+    constexpr int NQ = NA + NB, NMF = (BK / 16) * FM * FN;
+    constexpr int SP = (NMF * 3 / 4) / NQ > 0 ? (NMF * 3 / 4) / NQ : 1;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      if (ks + 1 < BK / 16) frag(ks + 1);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32<T>(bfr[j], af[i], acc[i][j]);
+        for (int j = 0; j < FN; ++j) {
+          acc[i][j] = mfma32<T>(bfr[ks & 1][j], af[ks & 1][i], acc[i][j]);
+          const int m = (ks * FM + i) * FN + j + 1;
+          if (m % SP == 0 && m / SP <= NQ && more) issue_one(kn % NST, kn, m / SP - 1);
+        }
+    }
+    if constexpr (NMF / SP < NQ) {
+#pragma unroll
+      for (int q = NMF / SP; q < NQ; ++q)
+        if (more) issue_one(kn % NST, kn, q);
     }
   }
 
@@ -414,9 +450,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
 }
 
 // Tile shape for the DMA kernel: minimise (tiles per CU, rounded up) x tile
-// area / relative efficiency. Candidates are 2-stage rings; the 128-row ones
-// fit two blocks per CU (<= 80 KB of LDS). SwiGLU needs whole [gate|up]
-// 64-column pairs per wave (FN even).
+// area / relative efficiency (one block per CU for every candidate). SwiGLU
+// needs whole [gate|up] 64-column pairs per wave (FN even).
 static int pick_dma_tile(int64_t M, int64_t N, bool swiglu, int cus) {
   struct Cand { int bm, bn, fn_wave; double eff; };
   // 128x128 / 128x192 / 128x256: 8 waves (4x2) of 32x64 / 32x96 / 32x128, so
