@@ -96,7 +96,8 @@ def test_linear_module_3d_input(dev):
 @pytest.mark.parametrize("n,k", [(3072, 1024), (1024, 3072), (4096, 1024), (1000, 200), (24, 2048)])
 def test_gemv_parity(dev, dtype, bsz, n, k):
     """[1x1024]@[1024x3072] and [1x3072]@[3072x1024]; plus the
-    decode-step shapes at batch 8/16 and ragged sizes (split-K workspace paths)."""
+    decode-step shapes at batch 8/16 and ragged sizes (a last row tile past N,
+    K shorter than one 256-wide wave batch)."""
     x, w, _ = _mk(bsz, n, k, dtype, seed=5)
     y = ext().gemv(x.to(dev), w.to(dev))
     close(y, oracle.gemv(x, w), what=f"gemv b{bsz} {n}x{k}")

@@ -159,6 +159,33 @@ def test_rope_params_fp64_closed_form():
     assert torch.all(cos[0] == 1) and torch.all(sin[0] == 0)
 
 
+def _rope_fixture():
+    import json
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "rope_params_d128_t1e6_s2048.json")
+    with open(path) as f:
+        return json.load(f)
+
+
+def test_rope_params_match_golden_fixture():
+    """The committed fp16 bit pattern of the D=128, theta=1e6, 2048-position
+    tables (tests/golden/make_rope_params.py): the oracle and the package's
+    own compute_rope_params on the CPU reproduce it bit for bit."""
+    import hashlib
+
+    from torchplusplus_amd.dlops import rope as R
+
+    fx = _rope_fixture()
+    rows = fx["rows"]
+    for name, (cos, sin) in [("oracle", oracle.compute_rope_params(128, 1e6, 2048)),
+                             ("package", R.compute_rope_params(128, 1e6, 2048, device="cpu"))]:
+        for t, key in [(cos, "cos"), (sin, "sin")]:
+            bits = t.contiguous().numpy().view(np.uint16)
+            assert hashlib.sha256(bits.astype("<u2").tobytes()).hexdigest() == fx["sha256_" + key], (name, key)
+            assert bits[rows].tolist() == fx[key + "_rows_u16"], (name, key)
+
+
 def test_rope_matches_complex_rotation():
     g = gen(9)
     d = 128
