@@ -124,6 +124,32 @@ def test_decode_shared_workspace_across_shapes(dev):
             close(decode_attention(q, kc, vc, lens), e, what=f"decode shape {i} pass {rep}")
 
 
+def test_decode_shared_workspace_across_streams(dev):
+    """Decode calls on two streams share the binding's per-device workspace;
+    each call waits for the stream that used it last, so back-to-back calls
+    on alternating streams stay correct."""
+    g = torch.Generator().manual_seed(12)
+    cases = []
+    for B, Lmax in [(8, 640), (4, 900)]:
+        q = torch.randn(B, 1, 16, 128, generator=g).bfloat16()
+        kc = torch.randn(B, 8, Lmax, 128, generator=g).bfloat16()
+        vc = torch.randn(B, 8, Lmax, 128, generator=g).bfloat16()
+        lens = torch.randint(Lmax // 2, Lmax + 1, (B,), generator=g, dtype=torch.int32)
+        cases.append(((q.to(dev), kc.to(dev), vc.to(dev), lens.to(dev)),
+                      oracle.decode_attention(q, kc, vc, lens.tolist())))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for rep in range(3):
+        for i, (args, _) in enumerate(cases):
+            with torch.cuda.stream(streams[(rep + i) % 2]):
+                outs.append((i, rep, decode_attention(*args)))
+    torch.cuda.synchronize()
+    for i, rep, o in outs:
+        close(o, cases[i][1], what=f"stream-alternating decode {i} pass {rep}")
+
+
 def test_decode_window_and_matches_prefill_path(dev):
     g = torch.Generator().manual_seed(8)
     B, Hq, Hkv, D, L = 3, 4, 2, 128, 300

@@ -429,24 +429,42 @@ std::vector<at::Tensor> gemv_argmax(at::Tensor input, at::Tensor weight,
 }
 
 // ---- attention (flash_attn_func contract) ----------------------------------
-// Per-device workspace for tpp_attn_decode, allocated once and reused, so a
-// captured decode graph keeps one stable pointer. Intentionally leaked: no
-// tensor destructor runs after the caching allocator is torn down at exit.
-// Zero-filled per-device scratch reused across calls on one stream. Slot 1
+// Zero-filled per-device scratch, allocated once and reused, so a captured
+// decode graph keeps one stable pointer (intentionally leaked: no tensor
+// destructor runs after the caching allocator is torn down at exit). Slot 1
 // belongs to decode attention alone: its arrival counters must stay zero
 // between calls, which the kernel guarantees but another user of the same
-// bytes would not.
+// bytes would not. Calls that share a slot must not overlap, so a call on a
+// stream other than the slot's last one first makes its stream wait for that
+// stream (an event); while a stream is being captured the capture is ordered
+// after earlier work by the caller (torch.cuda.graph synchronizes first).
+struct ScratchSlot {
+  at::Tensor t;
+  hipStream_t last = nullptr;
+  hipEvent_t ev = nullptr;
+};
+
 at::Tensor cached_workspace(const at::Tensor &like, size_t bytes, int slot = 0) {
-  static std::vector<at::Tensor> *cache = new std::vector<at::Tensor>(128);
+  static std::vector<ScratchSlot> *cache = new std::vector<ScratchSlot>(128);
   const int dev = like.device().index();
-  TORCH_CHECK(dev >= 0 && dev < 64, "device index out of range");
-  at::Tensor &ws = (*cache)[dev * 2 + slot];
-  if (!ws.defined() || (size_t)ws.numel() * 4 < bytes) {
+  TORCH_CHECK(dev >= 0 && dev < 64 && slot >= 0 && slot < 2, "device index out of range");
+  ScratchSlot &e = (*cache)[dev * 2 + slot];
+  hipStream_t s = (hipStream_t)cur_stream(like);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  TORCH_CHECK(hipStreamIsCapturing(s, &cs) == hipSuccess, "hipStreamIsCapturing failed");
+  const bool capturing = cs != hipStreamCaptureStatusNone;
+  if (!capturing && e.last && e.last != s) {
+    if (!e.ev) TORCH_CHECK(hipEventCreateWithFlags(&e.ev, hipEventDisableTiming) == hipSuccess, "hipEventCreate failed");
+    TORCH_CHECK(hipEventRecord(e.ev, e.last) == hipSuccess && hipStreamWaitEvent(s, e.ev, 0) == hipSuccess,
+                "ordering the shared workspace between streams failed");
+  }
+  if (!e.t.defined() || (size_t)e.t.numel() * 4 < bytes) {
     int64_t n = (int64_t)((bytes + 3) / 4);
     n = n < (1 << 20) ? (1 << 20) : n;
-    ws = torch::zeros({n}, like.options().dtype(at::kFloat));
+    e.t = torch::zeros({n}, like.options().dtype(at::kFloat));
   }
-  return ws;
+  e.last = capturing ? nullptr : s;
+  return e.t;
 }
 
 // greedy decode tail: ids <- argmax(lm_head(norm(input))), resid_next <-
