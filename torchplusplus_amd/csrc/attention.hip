@@ -542,31 +542,45 @@ constexpr int kDecBigNW = TPP_DEC_BIG_NW; // waves per block when G <= 2
 
 // RMSNorm (optional) + rotate-half RoPE of one head row held as 8 values per
 // lane by LPK lanes (lane dp owns d = 8 dp .. 8 dp + 7), rounded to T at the
-// same points as the unfused path (norm output, rotated output).
+// same points as the unfused path (norm output, rotated output). The norm
+// weights w and the table rows c, sn are passed in already loaded.
 template <typename T, int LPK>
-__device__ __forceinline__ void norm_rope_row(float (&x)[8], const T *nw, float eps,
-                                              const DecodeFuse &f, int pos, int dp) {
+__device__ __forceinline__ void norm_rope_vals(float (&x)[8], bool norm, const float (&w)[8],
+                                               float eps, const float (&c)[8],
+                                               const float (&sn)[8], int dp) {
   constexpr int D = LPK * 8;
-  if (nw) {
+  if (norm) {
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
     ss = group_sum<LPK>(ss);
     const float inv = rsqrtf(ss / (float)D + eps);
-    float w[8];
-    load8(nw + dp * 8, w);
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = to_f32(from_f32<T>((x[j] * inv) * w[j]));
   }
-  float pt[8], c[8], sn[8];
+  float pt[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) pt[j] = __shfl_xor(x[j], LPK / 2, kWave); // d +- D/2
-  const int pr = pos < 0 ? 0 : (pos < f.ctx ? pos : f.ctx - 1);
-  load_cs8_rt(f.cos, (int64_t)pr * D + dp * 8, f.cs_dtype, c);
-  load_cs8_rt(f.sin, (int64_t)pr * D + dp * 8, f.cs_dtype, sn);
   const float sgn = dp < LPK / 2 ? -1.f : 1.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) x[j] = to_f32(from_f32<T>(x[j] * c[j] + sgn * pt[j] * sn[j]));
+}
+
+// 8 RoPE table entries from 32 loaded bytes (fp32: lo then hi 16 bytes;
+// fp16 / bf16: the low 16 bytes), the table type a tpp_dtype code. All three
+// readings are formed and one selected, with no branch: a branch would let the
+// compiler sink the load of `hi` into it, and a load under a branch makes
+// every later wait a wait for all loads in flight.
+__device__ __forceinline__ void cs_vals(u32x4 lo, u32x4 hi, int cs_dtype, float (&v)[8]) {
+  const f16x8 h = __builtin_bit_cast(f16x8, lo);
+  const bf16x8 bh = __builtin_bit_cast(bf16x8, lo);
+  const bool f32 = cs_dtype == TPP_F32, f16t = cs_dtype == TPP_F16;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float a = __uint_as_float(i < 4 ? lo[i & 3] : hi[i & 3]);
+    const float b16 = f16t ? (float)h[i] : (float)bh[i];
+    v[i] = f32 ? a : b16;
+  }
 }
 
 template <typename T, int D, int G, int NW>
@@ -582,7 +596,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
   __shared__ float red_m[NW][G], red_l[NW][G];
   __shared__ float red_o[NW][G][D];
 
-  const int lane = lane_id(), w = wave_id();
+  // w through readfirstlane: the compiler then knows it (and every key index
+  // derived from it) is wave-uniform, so the key loop's exits are scalar
+  // branches rather than exec-mask updates with per-lane live-out copies
+  const int lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
   const int row = lane / LPK, dp = lane % LPK;
   int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   if (counters) {
@@ -595,6 +612,33 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
     hk = pair % p.Hkv;
     b = pair / p.Hkv;
   }
+  const T *kp = (const T *)p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + dp * 8;
+  const T *vp = (const T *)p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh + dp * 8;
+  // K/V rows of one batch of keys base + u*NW*KPW + row (u < U), each key
+  // clamped to `last`: past the keys a block scores they read a finite cache
+  // row whose scores compute_batch masks. Every batch is issued
+  // unconditionally: with no load under a branch the compiler's count of
+  // loads in flight stays exact, so scoring batch i waits for batch i only (a
+  // conditional load makes it wait for everything in flight).
+  constexpr int STRIDE = NW * KPW * U; // keys per block-wide batch
+  auto load_batch = [&](int base, int last, V8 (&kr)[U], V8 (&vr)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key0 = base + u * NW * KPW + row;
+      const int key = key0 < last ? key0 : last;
+      kr[u] = *reinterpret_cast<const V8 *>(kp + (int64_t)key * p.k_ss);
+      vr[u] = *reinterpret_cast<const V8 *>(vp + (int64_t)key * p.v_ss);
+    }
+  };
+  // The first two batches of the chunk go out before the sequence length is
+  // known (their keys depend on the block alone; clamped to the cache), so
+  // that round trip overlaps the first K/V loads. Three register sets: while
+  // one batch is scored the next two are in flight.
+  const int first = split * chunk + w * KPW;
+  V8 k0[U], v0[U], k1[U], v1[U], k2[U], v2[U];
+  load_batch(first, p.Sk - 1, k0, v0);
+  load_batch(first + STRIDE, p.Sk - 1, k1, v1);
+
   const int Lraw = seqlens ? seqlens[b] : fixed_len;
   const int L = Lraw < p.Sk ? (Lraw > 0 ? Lraw : 0) : p.Sk; // never read past the cache
   int lo = 0;
@@ -609,41 +653,73 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
   const bool own_new = fused && Lraw <= p.Sk && pnew >= k_begin && pnew < k_end;
   if (fused && k_end > pnew) k_end = pnew;
   const T *qkv_row = fused ? (const T *)fz.qkv + (int64_t)b * (p.Hq + 2 * p.Hkv) * D : nullptr;
-  const T *kp = (const T *)p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + dp * 8;
-  const T *vp = (const T *)p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh + dp * 8;
-  V8 zero;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) zero[i] = (T)0.0f;
 
-  // Software-pipelined key loop: the K/V loads of batch i+1 are in flight
-  // while batch i is scored, so a wave waits for memory once, not per batch.
-  constexpr int STRIDE = NW * KPW * U; // keys per block-wide batch
-  auto load_batch = [&](int base, V8 (&kr)[U], V8 (&vr)[U]) {
+  // Every load the prologue needs goes out next, unconditionally (an absent
+  // operand reads a valid row instead, never used): the q rows of the group,
+  // and when fused the norm weights, the RoPE rows at the new position and
+  // the new token's K/V row. One memory round trip then covers all of them
+  // and the first K/V batches, where a load under a branch, or a load whose
+  // address depends on an earlier one, costs a round trip each.
+  const T *qbase = fused ? qkv_row + (int64_t)hk * G * D
+                         : (const T *)p.q + (int64_t)b * p.q_sb + (int64_t)(hk * G) * p.q_sh;
+  const int64_t qstep = fused ? (int64_t)D : p.q_sh;
+  V8 q_raw[G];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int key = base + u * NW * KPW + row;
-      const bool ok = key < k_end;
-      kr[u] = ok ? *reinterpret_cast<const V8 *>(kp + (int64_t)key * p.k_ss) : zero;
-      vr[u] = ok ? *reinterpret_cast<const V8 *>(vp + (int64_t)key * p.v_ss) : zero;
-    }
-  };
-  // the first K/V batch is requested before the q prologue's dependent loads
-  const int first = k_begin + w * KPW;
-  V8 ka[U], va[U], kb[U], vb[U];
-  if (first < k_end) load_batch(first, ka, va);
+  for (int gi = 0; gi < G; ++gi) q_raw[gi] = *reinterpret_cast<const V8 *>(qbase + gi * qstep + dp * 8);
+  const T *anyrow = qbase + dp * 8;
+  const T *qw_src = fz.qw ? (const T *)fz.qw + dp * 8 : anyrow;
+  const T *kw_src = fz.kw ? (const T *)fz.kw + dp * 8 : anyrow;
+  const V8 qw_raw = *reinterpret_cast<const V8 *>(qw_src);
+  const V8 kw_raw = *reinterpret_cast<const V8 *>(kw_src);
+  const int pr = fused ? (pnew < 0 ? 0 : (pnew < fz.ctx ? pnew : fz.ctx - 1)) : 0;
+  const int64_t cs_es = fz.cs_dtype == TPP_F32 ? 4 : 2;
+  const char *c_src = fused ? (const char *)fz.cos + ((int64_t)pr * D + dp * 8) * cs_es
+                            : (const char *)anyrow;
+  const char *s_src = fused ? (const char *)fz.sin + ((int64_t)pr * D + dp * 8) * cs_es
+                            : (const char *)anyrow;
+  const int64_t cs_hi = fused && cs_es == 4 ? 16 : 0;
+  const u32x4 c_lo = *reinterpret_cast<const u32x4 *>(c_src);
+  const u32x4 c_hi = *reinterpret_cast<const u32x4 *>(c_src + cs_hi);
+  const u32x4 s_lo = *reinterpret_cast<const u32x4 *>(s_src);
+  const u32x4 s_hi = *reinterpret_cast<const u32x4 *>(s_src + cs_hi);
+  const V8 knew_raw =
+      *reinterpret_cast<const V8 *>(fused ? qkv_row + (int64_t)(p.Hq + hk) * D + dp * 8 : anyrow);
+  const V8 vnew_raw = *reinterpret_cast<const V8 *>(
+      fused ? qkv_row + (int64_t)(p.Hq + p.Hkv + hk) * D + dp * 8 : anyrow);
 
+  float c[8], sn[8];
+  cs_vals(c_lo, c_hi, fz.cs_dtype, c);
+  cs_vals(s_lo, s_hi, fz.cs_dtype, sn);
   float qv[G][8];
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qv[gi][j] = to_f32(q_raw[gi][j]);
     if (fused) {
-      load8(qkv_row + (int64_t)(hk * G + gi) * D + dp * 8, qv[gi]);
-      norm_rope_row<T, LPK>(qv[gi], (const T *)fz.qw, fz.eps, fz, pnew, dp);
-    } else {
-      const T *qp = (const T *)p.q + (int64_t)b * p.q_sb + (int64_t)(hk * G + gi) * p.q_sh + dp * 8;
-      load8(qp, qv[gi]);
+      float wq[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wq[j] = to_f32(qw_raw[j]);
+      norm_rope_vals<T, LPK>(qv[gi], fz.qw != nullptr, wq, fz.eps, c, sn, dp);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) qv[gi][j] *= p.scale_log2;
+  }
+  // the new token's K (normalised, rotated) and V, computed here by every
+  // wave and pinned (empty asm uses): left to the block that appends them
+  // they would keep their loads in flight across the whole key loop, and the
+  // registers the loop reuses would make every iteration wait for all loads
+  float kf[8], vf[8];
+  {
+    float wk[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      kf[j] = to_f32(knew_raw[j]);
+      vf[j] = to_f32(vnew_raw[j]);
+      wk[j] = to_f32(kw_raw[j]);
+    }
+    norm_rope_vals<T, LPK>(kf, fz.kw != nullptr, wk, fz.eps, c, sn, dp);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(kf[j]), "v"(vf[j]));
   }
   float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -657,7 +733,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
     float sc[U][G];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const bool ok = base + u * NW * KPW + row < k_end;
+      const bool ok = (unsigned)(base + u * NW * KPW + row - k_begin) < (unsigned)(k_end - k_begin);
       float kf[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) kf[j] = to_f32(kr[u][j]);
@@ -693,23 +769,35 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
       m[gi] = mb;
     }
   };
-  if (first < k_end) {
-    for (int base = first; base < k_end; base += 2 * STRIDE) {
-      const bool more = base + STRIDE < k_end;
-      if (more) load_batch(base + STRIDE, kb, vb);
-      compute_batch(base, ka, va);
-      if (!more) break;
-      if (base + 2 * STRIDE < k_end) load_batch(base + 2 * STRIDE, ka, va);
-      compute_batch(base + STRIDE, kb, vb);
-    }
+  // Whole triples of batches in the loop (a single exit: with a break after
+  // every batch the compiler merges the exits into one latch, whose state
+  // then has a batch in flight, and waits for everything at the loop head),
+  // the last one or two batches after it. Batches past the chunk that a
+  // triple loads are clamped rows and never scored.
+  // this wave's keys: first + i*STRIDE + u*NW*KPW + row, scored iff in
+  // [k_begin, k_end) (a window can start inside the chunk)
+  const int k_last = k_end > 0 ? k_end - 1 : 0;
+  int nbat = k_begin < k_end && first < k_end ? (k_end - first + STRIDE - 1) / STRIDE : 0;
+  int base = first;
+  for (; nbat >= 3; nbat -= 3, base += 3 * STRIDE) {
+    asm volatile("" ::: "memory");
+    load_batch(base + 2 * STRIDE, k_last, k2, v2);
+    asm volatile("" ::: "memory");
+    compute_batch(base, k0, v0);
+    asm volatile("" ::: "memory");
+    load_batch(base + 3 * STRIDE, k_last, k0, v0);
+    asm volatile("" ::: "memory");
+    compute_batch(base + STRIDE, k1, v1);
+    asm volatile("" ::: "memory");
+    load_batch(base + 4 * STRIDE, k_last, k1, v1);
+    asm volatile("" ::: "memory");
+    compute_batch(base + 2 * STRIDE, k2, v2);
   }
+  if (nbat >= 1) compute_batch(base, k0, v0);
+  if (nbat >= 2) compute_batch(base + STRIDE, k1, v1);
   if (own_new && w == 0) {
-    // the new key/value: normalise + rotate k, append both to the cache (row
-    // 0 lanes), and fold the key into row 0's online softmax
-    float kf[8], vf[8];
-    load8(qkv_row + (int64_t)(p.Hq + hk) * D + dp * 8, kf);
-    load8(qkv_row + (int64_t)(p.Hq + p.Hkv + hk) * D + dp * 8, vf);
-    norm_rope_row<T, LPK>(kf, (const T *)fz.kw, fz.eps, fz, pnew, dp);
+    // the new key/value (normalised and rotated in the prologue): append both
+    // to the cache (row 0 lanes) and fold the key into row 0's online softmax
     if (row == 0) {
       store8((T *)kp + (int64_t)pnew * p.k_ss, kf);
       store8((T *)vp + (int64_t)pnew * p.v_ss, vf);
@@ -730,24 +818,39 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
       }
     }
   }
-  // merge the KPW key rows of the wave (lanes with equal dp)
+  // merge the KPW key rows of the wave (lanes with equal dp): at distance
+  // SH = LPK .. 32 every lane gets its own and its partner's (m, l, acc) as an
+  // unordered pair (v_permlane16/32_swap, or a row rotation by 8), and
+  // combines them symmetrically, so both lanes of a pair get the same value
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) {
-#pragma unroll
-    for (int sh = LPK; sh < kWave; sh <<= 1) {
-      const float mo = __shfl_xor(m[gi], sh, kWave);
-      const float lo2 = __shfl_xor(l[gi], sh, kWave);
-      const float mn = fmaxf(m[gi], mo);
+    auto merge_at = [&](auto pair_of) {
+      float ma, mb, la, lb;
+      pair_of(m[gi], ma, mb);
+      pair_of(l[gi], la, lb);
+      const float mn = fmaxf(ma, mb);
       const float mu = mn == -INFINITY ? 0.f : mn;
-      const float a = exp2f(m[gi] - mu), c = exp2f(mo - mu);
-      l[gi] = l[gi] * a + lo2 * c;
+      const float a = exp2f(ma - mu), c = exp2f(mb - mu);
+      l[gi] = la * a + lb * c;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float ao = __shfl_xor(acc[gi][j], sh, kWave);
-        acc[gi][j] = acc[gi][j] * a + ao * c;
+        float xa, xb;
+        pair_of(acc[gi][j], xa, xb);
+        acc[gi][j] = xa * a + xb * c;
       }
       m[gi] = mn;
-    }
+    };
+    if constexpr (LPK <= 8)
+      merge_at([](float x, float &a, float &b) { a = x, b = dpp_f32<kDppRowRor8>(x); });
+    if constexpr (LPK <= 16)
+      merge_at([](float x, float &a, float &b) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+      });
+    merge_at([](float x, float &a, float &b) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+      a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+    });
     if (row == 0) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) red_o[w][gi][dp * 8 + j] = acc[gi][j];
@@ -816,15 +919,37 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int gi = idx / D, d = idx % D;
     const float *sl = ws_o + (((int64_t)b * p.Hq + hk * G + gi) * nsplit) * (D + 32);
-    float mx = -INFINITY;
-    for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, sl[sp * (D + 32) + D]);
-    const float mu = mx == -INFINITY ? 0.f : mx;
-    float ls = 0.f, os = 0.f;
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const float *q = sl + sp * (D + 32);
-      const float wgt = exp2f(q[D] - mu);
-      ls += wgt * q[D + 1];
-      os += wgt * q[d];
+    // the partials in groups of MG splits: a group's loads all go out before
+    // any is used (indices past nsplit read the last split and weigh 0), one
+    // L2 round trip per group instead of two per split; groups after the
+    // first rescale the running sums (online softmax)
+    constexpr int MG = 8;
+    float mu = -INFINITY, ls = 0.f, os = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += MG) {
+      float mv[MG], lv[MG], ov[MG];
+#pragma unroll
+      for (int j = 0; j < MG; ++j) {
+        const int sp = s0 + j < nsplit ? s0 + j : nsplit - 1;
+        const float *q = sl + (int64_t)sp * (D + 32);
+        mv[j] = q[D];
+        lv[j] = q[D + 1];
+        ov[j] = q[d];
+      }
+      float mx = mu;
+#pragma unroll
+      for (int j = 0; j < MG; ++j)
+        if (s0 + j < nsplit) mx = fmaxf(mx, mv[j]);
+      const float mn = mx == -INFINITY ? 0.f : mx;
+      const float a = mu == -INFINITY ? 0.f : exp2f(mu - mn);
+      ls *= a;
+      os *= a;
+#pragma unroll
+      for (int j = 0; j < MG; ++j) {
+        const float wgt = s0 + j < nsplit ? exp2f(mv[j] - mn) : 0.f;
+        ls += wgt * lv[j];
+        os += wgt * ov[j];
+      }
+      mu = mx;
     }
     T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)(hk * G + gi) * p.o_sh;
     op[d] = from_f32<T>(ls > 0.f ? os / ls : 0.f);
@@ -1073,6 +1198,8 @@ static int decode_impl(const char *name, AttnArgs &a, int64_t D, int64_t Lmax,
                        size_t ws_bytes, void *stream) {
   if (int e = check_attn(name, a, D)) return e;
   if (a.B == 0) return TPP_OK;
+  // the kernel reads cache row 0 even for empty sequences (clamped loads)
+  if (Lmax < 1) return set_error(TPP_E_INVALID, "%s: the cache must hold at least one row", name);
   if (D != 64 && D != 128)
     return set_error(TPP_E_UNSUPPORTED, "%s: head_dim %lld not in {64, 128}", name, (long long)D);
   if (a.Hq / a.Hkv > kDecMaxG)
