@@ -33,14 +33,24 @@ enum GemvEpi { kEpiPlain = 0, kEpiBiasAct = 1, kEpiSwiGLU = 2, kEpiResidual = 3 
 constexpr int kGemvWaveK = 256;   // K elements per wave and load batch
 constexpr int kGemvMaxWaves = 12; // 768 threads: 170 VGPRs per lane, no spills
 
+// 16 zero bytes in device memory (zero-initialised, never written): what a
+// skipped load reads instead. Not const: a pointer into the constant address
+// space mixed with global ones would turn every such load into a flat load.
+__device__ uint32_t g_gemv_zero16[4];
+
+// 16-byte load of 8 elements, zero unless ok. The load is always issued, from
+// the zero bytes when !ok: a load under a branch makes the compiler's later
+// waits drain every load in flight (one memory round trip becomes several),
+// and selecting the value after the load would wait for it on the spot.
 template <typename T>
 __device__ __forceinline__ typename VecT<T>::v8 ld16(const T *p, bool ok) {
   typedef typename VecT<T>::v8 V;
-  if (ok) return *reinterpret_cast<const V *>(p);
-  V z;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) z[i] = (T)0.0f;
-  return z;
+  return *reinterpret_cast<const V *>(ok ? p : reinterpret_cast<const T *>(g_gemv_zero16));
+}
+// one element the same way
+template <typename T>
+__device__ __forceinline__ float ld1(const T *p, bool ok) {
+  return to_f32(*(ok ? p : reinterpret_cast<const T *>(g_gemv_zero16)));
 }
 
 template <typename T>
@@ -140,12 +150,12 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       if constexpr (EPI == kEpiSwiGLU) b1[u] = ld16(w1 + c, in && w1ok);
     }
     if constexpr (EPI == kEpiResidual) {
-      if (w == 0 && row0 + r < N) {
+      // every wave loads (branch-free); wave 0's values are the ones used
+      const T *rs = (const T *)a.residual;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int b = 4 * g + i;
-          if (b < a.NB) res[i] = to_f32(((const T *)a.residual)[(int64_t)b * a.ldy + row0 + r]);
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int b = 4 * g + i;
+        res[i] = ld1(rs + (int64_t)b * a.ldy + row0 + r, row0 + r < N && b < a.NB);
       }
     }
   };
@@ -181,12 +191,12 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       }
     }
     if constexpr (EPI == kEpiResidual) {
-      if (w == 0 && row0 + r < N) {
+      // every wave loads (branch-free); wave 0's values are the ones used
+      const T *rs = (const T *)a.residual;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int b = 4 * g + i;
-          if (b < a.NB) res[i] = to_f32(((const T *)a.residual)[(int64_t)b * a.ldy + row0 + r]);
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int b = 4 * g + i;
+        res[i] = ld1(rs + (int64_t)b * a.ldy + row0 + r, row0 + r < N && b < a.NB);
       }
     }
   };
@@ -217,15 +227,12 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       const bool ok = c < k_end && xok;
       dst[u] = ld16(xr + c, ok);
       if constexpr (NORM) {
-        if (ok) {
-          float xv[8], nv[8];
+        // zero where !ok: both factors are zero there
+        const V8 nw8 = ld16((const T *)a.norm_w + c, ok);
+        const float inv = s_inv[r];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) xv[i] = to_f32(dst[u][i]);
-          load8((const T *)a.norm_w + c, nv);
-          const float inv = s_inv[r];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) dst[u][i] = from_f32<T>((xv[i] * inv) * nv[i]);
-        }
+        for (int i = 0; i < 8; ++i)
+          dst[u][i] = from_f32<T>((to_f32(dst[u][i]) * inv) * to_f32(nw8[i]));
       }
     }
   };
@@ -241,6 +248,9 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
         xa[u] = ld16(xr + c, c < k_end && xok);
         nwv[u] = ld16((const T *)a.norm_w + c, c < k_end);
       }
+      // all loads out before the first use (the scheduler would otherwise
+      // start the sums on the first row chunk and wait for it mid-issue)
+      __builtin_amdgcn_sched_barrier(0);
       float ss = 0.f;
 #pragma unroll
       for (int u = 0; u < NS; ++u)
@@ -581,13 +591,11 @@ __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tile
     const bool ok = c < K && xok;
     xa[u] = ld16(xr + c, ok);
     if constexpr (NORM) {
-      if (ok) {
-        float nv[8];
-        load8((const T *)a.norm_w + c, nv);
-        const float inv = s_inv[r];
+      // zero where !ok: both factors are zero there
+      const V8 nw8 = ld16((const T *)a.norm_w + c, ok);
+      const float inv = s_inv[r];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xa[u][i] = from_f32<T>((to_f32(xa[u][i]) * inv) * nv[i]);
-      }
+      for (int i = 0; i < 8; ++i) xa[u][i] = from_f32<T>((to_f32(xa[u][i]) * inv) * to_f32(nw8[i]));
     }
   }
 
