@@ -36,40 +36,38 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
   const int64_t row =
       ((int64_t)blockIdx.x * (blockDim.x / kWave) + wave_id()) * RPW + sub;
   const bool valid = row < M;
+  const int64_t rowc = valid ? row : M - 1; // launched only for M >= 1
   const int nvec = N >> 3;
 
-  // the weight (and bias) chunks are requested together with x, so the
-  // output pass after the row reduction waits on no further memory
+  // Every load of the row goes out first and unconditionally: chunks past the
+  // row and rows past M read chunk nvec-1 / row M-1 (values discarded), so the
+  // compiler's count of loads in flight stays exact and the row costs one
+  // memory round trip (a load under a branch makes the next wait drain every
+  // load, one round trip per chunk). The weight (and bias) chunks go with x,
+  // so the output pass waits on no further memory.
   typedef typename VecT<T>::v8 V8;
   constexpr bool kOut = (MODE == kRms || MODE == kLayer || MODE == kAddRms);
-  V8 wr[MAXV], br[MAXV];
-  if constexpr (kOut) {
+  V8 xr[MAXV], rr[MAXV], wr[MAXV], br[MAXV];
 #pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-      const int c = j * LPR + l;
-      if (valid && c < nvec) {
-        wr[j] = *reinterpret_cast<const V8 *>(w + (int64_t)c * 8);
-        if (MODE == kLayer && b) br[j] = *reinterpret_cast<const V8 *>(b + (int64_t)c * 8);
-      }
-    }
+  for (int j = 0; j < MAXV; ++j) {
+    const int c = j * LPR + l;
+    const int64_t cc = (int64_t)(c < nvec ? c : nvec - 1) * 8;
+    xr[j] = *reinterpret_cast<const V8 *>(x + rowc * ldx + cc);
+    if constexpr (MODE == kAddRms) rr[j] = *reinterpret_cast<const V8 *>(resid + rowc * ldy + cc);
+    if constexpr (kOut) wr[j] = *reinterpret_cast<const V8 *>(w + cc);
+    if constexpr (MODE == kLayer) br[j] = *reinterpret_cast<const V8 *>((b ? b : w) + cc);
   }
+  __builtin_amdgcn_sched_barrier(0);
   float v[MAXV][8];
   float sum = 0.f;
 #pragma unroll
   for (int j = 0; j < MAXV; ++j) {
-    const int c = j * LPR + l;
-    if (valid && c < nvec) {
-      load8(x + row * ldx + (int64_t)c * 8, v[j]);
-      if constexpr (MODE == kAddRms) {
-        float r[8];
-        load8(resid + row * ldy + (int64_t)c * 8, r);
+    const bool ok = valid && j * LPR + l < nvec;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[j][i] = to_f32(from_f32<T>(v[j][i] + r[i]));
-        store8(resid + row * ldy + (int64_t)c * 8, v[j]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[j][i] = 0.f;
+    for (int i = 0; i < 8; ++i) {
+      float xv = to_f32(xr[j][i]);
+      if constexpr (MODE == kAddRms) xv = to_f32(from_f32<T>(xv + to_f32(rr[j][i])));
+      v[j][i] = ok ? xv : 0.f;
     }
     if constexpr (MODE == kLayer || MODE == kLayerStats) {
 #pragma unroll
@@ -101,6 +99,16 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
   } else {
     scale = rsqrtf(sum / (float)N + eps);
   }
+  if constexpr (kOut) {
+    // used only inside the per-chunk store branches below: pinned here so
+    // the compiler cannot sink their loads into those branches (a second
+    // memory round trip after the reduction)
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      asm volatile("" ::"v"(wr[j]));
+      if constexpr (MODE == kLayer) asm volatile("" ::"v"(br[j]));
+    }
+  }
   if (!valid) return;
 
   if constexpr (MODE == kRmsStats) {
@@ -128,6 +136,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
 #pragma unroll
           for (int i = 0; i < 8; ++i) o[i] = (v[j][i] * scale) * to_f32(wr[j][i]);
         }
+        if constexpr (MODE == kAddRms) store8(resid + row * ldy + (int64_t)c * 8, v[j]);
         store8(y + row * ldy + (int64_t)c * 8, o);
       }
     }
@@ -224,7 +233,10 @@ static int launch_norm(const void *x_, const void *w_, const void *b_, void *y_,
     } else {
       const int64_t rows_per_block = 4;
       dim3 grid((unsigned)((M + rows_per_block - 1) / rows_per_block));
-      if (N <= 2048)
+      if (N <= 1024)
+        norm_rows_kernel<T, 64, 2, MODE><<<grid, block, 0, st>>>(
+            x, w, b, y, r, s0, s1, M, (int)N, ldx, ldy, eps);
+      else if (N <= 2048)
         norm_rows_kernel<T, 64, 4, MODE><<<grid, block, 0, st>>>(
             x, w, b, y, r, s0, s1, M, (int)N, ldx, ldy, eps);
       else
