@@ -236,11 +236,17 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
   // S^T = K Q^T for the K tile in slot buf. The K fragments of step ks + 2
   // are requested before the MFMAs of step ks (scheduling barriers keep the
   // compiler from pulling the reads back next to their use), so LDS latency
-  // hides behind the matrix work.
+  // hides behind the matrix work. The reads are inline asm with explicit
+  // waits, like the V reads (from plain LDS loads the compiler waited for
+  // all outstanding reads every third step).
   auto qk = [&](int buf) {
-    auto kfrag = [&](int ks, int st) {
-      const int key = st * 32 + ql, ch = ks * 2 + h;
-      return sm.k[buf][key * CPR + (ch ^ (key & (CPR - 1)))];
+    const unsigned kbase = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char *)&sm.k[buf][0];
+    // step ks, key row st * 32 + ql: the st = 1 row is 32 rows (32 * D * 2
+    // bytes) after the st = 0 row, with the same swizzle
+    auto kfrag = [&](int ks, V8 (&dst)[2]) {
+      const unsigned a = kbase + (unsigned)((ql * CPR + ((ks * 2 + h) ^ (ql & (CPR - 1)))) * 16);
+      dst[0] = lds_read_b128<0, V8>(a);
+      dst[1] = lds_read_b128<32 * D * 2, V8>(a);
     };
     constexpr int KS = D / 16;
     V8 kr[3][2];
@@ -250,23 +256,20 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
       for (int st = 0; st < 2; ++st)
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[g][st][r] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int st = 0; st < 2; ++st) kr[ks][st] = kfrag(ks, st);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if (ks + 2 < KS) {
-#pragma unroll
-        for (int st = 0; st < 2; ++st) kr[(ks + 2) % 3][st] = kfrag(ks + 2, st);
-      }
+    kfrag(0, kr[0]);
+    kfrag(1, kr[1]);
+    static_for<KS>([&](auto kk) {
+      constexpr int ks = decltype(kk)::value;
+      if constexpr (ks + 2 < KS) kfrag(ks + 2, kr[(ks + 2) % 3]);
+      // the reads of steps ks + 1, ks + 2 stay in flight
+      lds_wait_tied<(ks + 2 < KS ? 2 : KS - 1 - ks) * 2>(kr[ks % 3]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
         for (int g = 0; g < QG; ++g) s[g][st] = mfma32x32<T>(kr[ks % 3][st], qf[g][ks], s[g][st]);
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
   };
 
   // Online softmax on raw scores of tile t: the running max m is kept
@@ -365,42 +368,53 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
   // 16c + 8 + 4h + 0..3 (second), the key order of the score registers (P
   // stays the B operand unchanged). The V fragments of step c + 2 are
   // requested before the MFMAs of step c.
+  //
+  // Key rows 16c + kl and 16c + kl + 8 (kl = 4(grp/2) + c4 < 16) have the
+  // swizzle of kl, so a lane's address for step c is its step-0 address plus
+  // the constant 32cD bytes (+16D for the second read): one base register per
+  // 32-column slab, the step in the instruction's offset.
   auto pv = [&](int buf) {
-    typedef short s16x4 __attribute__((ext_vector_type(4)));
     typedef short s16x8 __attribute__((ext_vector_type(8)));
+    constexpr int R = 2 * NT; // LDS reads per 16-key step
     const int grp = lane >> 4, a4 = lane & 3, c4 = (lane >> 2) & 3;
-    const __attribute__((address_space(3))) char *vbase =
-        (const __attribute__((address_space(3))) char *)&sm.v[buf][0];
-    auto vfrag = [&](int c, int tt) {
-      const int key1 = 16 * c + 4 * (grp >> 1) + c4, key2 = key1 + 8;
+    const int kl = 4 * (grp >> 1) + c4;
+    const unsigned vbase = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char *)&sm.v[buf][0];
+    unsigned vb[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
       const int d0 = tt * 32 + 16 * (grp & 1) + 4 * a4; // this lane's 4 columns
-      const int o1 = key1 * D * 2 + (((d0 >> 3) ^ vswz<D>(key1)) << 4) + ((d0 & 7) << 1);
-      const int o2 = key2 * D * 2 + (((d0 >> 3) ^ vswz<D>(key2)) << 4) + ((d0 & 7) << 1);
-      const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4 *)(vbase + o1));
-      const s16x4 r2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4 *)(vbase + o2));
-      const s16x8 r12 = __builtin_shufflevector(r1, r2, 0, 1, 2, 3, 4, 5, 6, 7);
-      return __builtin_bit_cast(V8, r12);
+      vb[tt] = vbase + kl * D * 2 + (((d0 >> 3) ^ vswz<D>(kl)) << 4) + ((d0 & 7) << 1);
+    }
+    s16x4 vr[3][R];
+    auto vfrag = [&](auto cc) {
+      constexpr int c = decltype(cc)::value;
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) {
+        vr[c % 3][2 * tt] = lds_read_tr16<c * 32 * D>(vb[tt]);
+        vr[c % 3][2 * tt + 1] = lds_read_tr16<c * 32 * D + 16 * D>(vb[tt]);
+      }
     };
-    V8 vr[3][NT];
+    auto step = [&](auto cc) {
+      constexpr int c = decltype(cc)::value;
+      if constexpr (c + 2 < 4) vfrag(std::integral_constant<int, c + 2>{});
+      // reads of the later steps already issued stay in flight (LDS reads
+      // complete in order)
+      constexpr int later = (c + 2 < 4 ? 2 : 3 - c) * R;
+      lds_wait_tied<later>(vr[c % 3]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+      for (int tt = 0; tt < NT; ++tt) {
+        const s16x8 r12 = __builtin_shufflevector(vr[c % 3][2 * tt], vr[c % 3][2 * tt + 1], 0, 1,
+                                                  2, 3, 4, 5, 6, 7);
+        const V8 a = __builtin_bit_cast(V8, r12);
 #pragma unroll
-      for (int tt = 0; tt < NT; ++tt) vr[c][tt] = vfrag(c, tt);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (c + 2 < 4) {
-#pragma unroll
-        for (int tt = 0; tt < NT; ++tt) vr[(c + 2) % 3][tt] = vfrag(c + 2, tt);
+        for (int g = 0; g < QG; ++g) o[g][tt] = mfma32x32<T>(a, pb[g][c], o[g][tt]);
       }
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int tt = 0; tt < NT; ++tt)
-#pragma unroll
-        for (int g = 0; g < QG; ++g) o[g][tt] = mfma32x32<T>(vr[c % 3][tt], pb[g][c], o[g][tt]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    };
+    vfrag(std::integral_constant<int, 0>{});
+    vfrag(std::integral_constant<int, 1>{});
+    static_for<4>(step);
   };
 
   // Slots: K tile t and V tile t live in slot (t - t_begin) & 1. The leading

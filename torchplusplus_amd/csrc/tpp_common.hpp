@@ -10,6 +10,8 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <type_traits>
+#include <utility>
 
 #include "../../include/tpp.h"
 
@@ -186,6 +188,64 @@ __host__ __device__ inline bool aligned16(const void *p) { return (reinterpret_c
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 inline int elem_size(int dtype) { return dtype == TPP_F32 ? 4 : 2; }
 inline bool half_type(int dtype) { return dtype == TPP_F16 || dtype == TPP_BF16; }
+
+// LDS reads as inline asm, at byte address addr + OFF. The compiler's
+// wait-count pass does not see them, so the caller waits for the results
+// with lds_wait_tied. Where the pass does see them it over-waits: the
+// transposing read's builtin carries no alias information, so it waits for
+// every LDS-DMA in flight (vmcnt(0)), including DMA into other slots; and
+// fragment reads a few steps ahead of their MFMAs get lgkmcnt(0) waits that
+// also cover the reads still meant to be in flight.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+template <int OFF> __device__ __forceinline__ s16x4 lds_read_tr16(unsigned addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  s16x4 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+template <int OFF, typename V> __device__ __forceinline__ V lds_read_b128(unsigned addr) {
+  static_assert(OFF >= 0 && OFF < 65536 && sizeof(V) == 16, "ds offset is 16 bits");
+  V r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+// s_waitcnt lgkmcnt(N) that also redefines the results in v, which are
+// complete once at most N LDS reads are outstanding: uses of v after it see
+// the loaded data (the tie keeps the compiler from copying a register the
+// load has not yet written before the wait). LDS reads complete in order.
+template <int N, typename V, int M> __device__ __forceinline__ void lds_wait_tied(V (&v)[M]) {
+  static_assert(N >= 0, "lgkmcnt");
+  constexpr int n = N < 15 ? N : 15; // 4-bit field: a smaller count only waits longer
+  if constexpr (M == 2)
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(v[0]), "+v"(v[1]) : "n"(n));
+  else if constexpr (M == 3)
+    asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]) : "n"(n));
+  else if constexpr (M == 4)
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "n"(n));
+  else if constexpr (M == 5)
+    asm volatile("s_waitcnt lgkmcnt(%5)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4])
+                 : "n"(n));
+  else if constexpr (M == 6)
+    asm volatile("s_waitcnt lgkmcnt(%6)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5])
+                 : "n"(n));
+  else if constexpr (M == 8)
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7])
+                 : "n"(n));
+  else
+    static_assert(M >= 2 && M <= 8 && M != 7, "2 to 6 or 8 registers");
+}
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, in order
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F> __device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 } // namespace tpp
 
