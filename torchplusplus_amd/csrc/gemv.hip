@@ -47,10 +47,31 @@ __device__ __forceinline__ typename VecT<T>::v8 ld16(const T *p, bool ok) {
   typedef typename VecT<T>::v8 V;
   return *reinterpret_cast<const V *>(ok ? p : reinterpret_cast<const T *>(g_gemv_zero16));
 }
-// one element the same way
+// 16 bytes the same way as inline asm, invisible to the compiler's wait
+// counts: the caller waits with vm_wait_tied
 template <typename T>
-__device__ __forceinline__ float ld1(const T *p, bool ok) {
-  return to_f32(*(ok ? p : reinterpret_cast<const T *>(g_gemv_zero16)));
+__device__ __forceinline__ typename VecT<T>::v8 ld16_asm(const T *p, bool ok) {
+  typename VecT<T>::v8 r;
+  const void *q = ok ? (const void *)p : (const void *)g_gemv_zero16;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(q));
+  return r;
+}
+// s_waitcnt vmcnt(N) that also redefines the loaded registers (see
+// lds_wait_tied): a and b complete once at most N later loads are in flight
+template <int N, typename V>
+__device__ __forceinline__ void vm_wait_tied(V (&a)[8], V (&b)[8]) {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%16)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]),
+                 "+v"(a[6]), "+v"(a[7]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]),
+                 "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7])
+               : "n"(N));
+}
+// one element the same way, returned unconverted: a conversion next to the
+// load would make the wave wait for it (and every load before it) there
+template <typename T>
+__device__ __forceinline__ T ld1(const T *p, bool ok) {
+  return *(ok ? p : reinterpret_cast<const T *>(g_gemv_zero16));
 }
 
 template <typename T>
@@ -135,7 +156,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   };
   // W of one tile for this wave's K batch at k, plus the residual values
   // the tile will update
-  auto load_w = [&](int64_t tile, int64_t k, V8 (&b0)[NS], V8 (&b1)[NS], float (&res)[4]) {
+  auto load_w = [&](int64_t tile, int64_t k, V8 (&b0)[NS], V8 (&b1)[NS], T (&res)[4]) {
     int64_t row0, row1;
     rows_of(tile, row0, row1);
     const bool w0ok = row0 + r < N;
@@ -167,13 +188,15 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   // into the MFMA layout (16 rows x 64 bytes per instruction) the same
   // weights stream at about a quarter of the rate per CU. Rows past N read
   // row N-1 and units past K read the last unit (finite data, multiplied by
-  // x = 0 or discarded). With the fused RMSNorm the first tile's DMA is
-  // issued before the input prologue, so the two latency chains overlap.
+  // x = 0 or discarded). The first tile's DMA is issued right after the
+  // input loads (every block has a first tile): the two are in flight
+  // together, and since loads complete in issue order the input can be used
+  // (row statistics, normalisation) while the weights are still on the way.
   constexpr int NSET = EPI == kEpiSwiGLU ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) char gemv_smem[];
   V8 *wslot = reinterpret_cast<V8 *>(gemv_smem) + (size_t)w * NSET * (16 * 32);
   const int drow = lane >> 5, dpos = lane & 31;
-  auto issue_w = [&](int64_t tile, float (&res)[4]) {
+  auto issue_w = [&](int64_t tile, T (&res)[4]) {
     int64_t row0, row1;
     rows_of(tile, row0, row1);
 #pragma unroll
@@ -213,8 +236,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   };
   const bool x_res = k_end - k_begin <= kGemvWaveK;
   V8 pa0[NS], pa1[NS];
-  float ra[4] = {0.f, 0.f, 0.f, 0.f};
-  if (NORM && x_res && blockIdx.x < tiles) issue_w(blockIdx.x, ra);
+  T ra[4] = {};
 
   // this wave's slice of the (normalised) input, reused by every tile
   // kept resident when the wave's K slice is one load batch (K <= 4096 for
@@ -245,12 +267,18 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
 #pragma unroll
       for (int u = 0; u < NS; ++u) {
         const int64_t c = k_begin + u * 32 + g * 8;
-        xa[u] = ld16(xr + c, c < k_end && xok);
-        nwv[u] = ld16((const T *)a.norm_w + c, c < k_end);
+        xa[u] = ld16_asm(xr + c, c < k_end && xok);
+        nwv[u] = ld16_asm((const T *)a.norm_w + c, c < k_end);
       }
-      // all loads out before the first use (the scheduler would otherwise
-      // start the sums on the first row chunk and wait for it mid-issue)
       __builtin_amdgcn_sched_barrier(0);
+      issue_w(blockIdx.x, ra);
+      // all loads out before the first use (the scheduler would otherwise
+      // start the sums on the first row chunk and wait for it mid-issue);
+      // the weight DMA (and residual loads) issued after the input stay in
+      // flight: the input loads are asm, since after an LDS-DMA the
+      // compiler's own wait for a plain load is vmcnt(0)
+      __builtin_amdgcn_sched_barrier(0);
+      vm_wait_tied<8 * NSET + (EPI == kEpiResidual ? 4 : 0)>(xa, nwv);
       float ss = 0.f;
 #pragma unroll
       for (int u = 0; u < NS; ++u)
@@ -262,7 +290,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       ss += __shfl_xor(ss, 16, kWave); // lanes r, r+16, r+32, r+48: row r
       ss += __shfl_xor(ss, 32, kWave);
       if (g == 0) s_part[w][r] = ss;
-      __syncthreads();
+      lds_barrier(); // (a fenced barrier would also wait for the weight DMA)
       float tot = 0.f;
       for (int i = 0; i < nw; ++i) tot += s_part[i][r];
       const float inv = rsqrtf(tot / (float)K + a.eps);
@@ -289,7 +317,8 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
     }
   } else if (x_res) {
     load_x(k_begin, xa);
-    if (blockIdx.x < tiles) issue_w(blockIdx.x, ra);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_w(blockIdx.x, ra);
   }
 
   // per-block running argmax over all tiles (wave 0, lanes r == 0 hold it)
@@ -297,12 +326,12 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   int am_i[4] = {0x7fffffff, 0x7fffffff, 0x7fffffff, 0x7fffffff};
 
   // block-wide K reduction of a tile's accumulators and its epilogue
-  auto finish = [&](int64_t tile, f32x4 acc0, f32x4 acc1, const float (&res_in)[4]) {
+  auto finish = [&](int64_t tile, f32x4 acc0, f32x4 acc1, const T (&res_in)[4]) {
     int64_t row0, row1;
     rows_of(tile, row0, row1);
     red[0][w][lane] = acc0;
     if constexpr (EPI == kEpiSwiGLU) red[1][w][lane] = acc1;
-    __syncthreads();
+    lds_barrier(); // the next tile's weight DMA stays in flight
     if (w == 0) {
       acc0 = red[0][0][lane];
       for (int i = 1; i < nw; ++i) acc0 += red[0][i][lane];
@@ -339,7 +368,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
         } else if (n0 < N) {
           if constexpr (EPI == kEpiResidual) {
             const float v = to_f32(from_f32<T>(acc0[i]));
-            ((T *)a.residual)[(int64_t)b * a.ldy + n0] = from_f32<T>(res_in[i] + v);
+            ((T *)a.residual)[(int64_t)b * a.ldy + n0] = from_f32<T>(to_f32(res_in[i]) + v);
           } else if constexpr (EPI == kEpiBiasAct) {
             Y[(int64_t)b * a.ldy + n0] = epi_bias_act<T, ACT>(acc0[i], (const T *)a.bias, n0);
           } else if (Y) {
@@ -348,7 +377,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
         }
       }
     }
-    __syncthreads(); // red[] is reused by the next tile
+    lds_barrier(); // red[] is reused by the next tile
   };
   auto mfma_batch = [&](const V8 (&xv)[NS], const V8 (&b0)[NS], const V8 (&b1)[NS], f32x4 &acc0,
                         f32x4 &acc1) {
@@ -365,7 +394,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
     // t + stride fills the slot
     for (int64_t t = blockIdx.x; t < tiles; t += stride) {
       fetch_w(pa0, pa1);
-      float rc[4] = {ra[0], ra[1], ra[2], ra[3]};
+      T rc[4] = {ra[0], ra[1], ra[2], ra[3]};
       if (t + stride < tiles) issue_w(t + stride, ra);
       f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
       mfma_batch(xa, pa0, pa1, c0, c1);
@@ -374,7 +403,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   } else {
     for (int64_t tile = blockIdx.x; tile < tiles; tile += stride) {
       f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
-      float res[4] = {0.f, 0.f, 0.f, 0.f};
+      T res[4] = {};
       for (int64_t k = k_begin; k < k_end; k += kGemvWaveK) {
         V8 b0[NS], b1[NS], xl[NS];
         load_w(tile, k, b0, b1, res);

@@ -189,6 +189,16 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 inline int elem_size(int dtype) { return dtype == TPP_F32 ? 4 : 2; }
 inline bool half_type(int dtype) { return dtype == TPP_F16 || dtype == TPP_BF16; }
 
+// Workgroup barrier for data exchanged through LDS by ds_write/ds_read: waits
+// for this wave's LDS accesses (lgkmcnt(0)) but, unlike the fenced
+// __syncthreads(), not for LDS-DMA (global_load_lds) still in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // LDS reads as inline asm, at byte address addr + OFF. The compiler's
 // wait-count pass does not see them, so the caller waits for the results
 // with lds_wait_tied. Where the pass does see them it over-waits: the
