@@ -557,7 +557,6 @@ template <typename T, bool NORM, int KC>
 __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tiles) {
   typedef typename VecT<T>::v8 V8;
   __shared__ V8 ring[4][kWideRing][16 * 32]; // [wave][slot][row * 32 + (unit ^ row)]
-  __shared__ float s_inv[16];
   __shared__ float s_bv[4][16];
   __shared__ int s_bi[4][16];
   const int lane = lane_id(), w = wave_id();
@@ -595,36 +594,43 @@ __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tile
     for (int p = 0; p < kWideRing - 1; ++p) issue(p);
   }
 
-  // input rows (<= 16) as A fragments for all K: step u covers k = 32u + 8g
-  if constexpr (NORM) {
-    for (int row = w; row < a.NB; row += 4) {
-      const T *xp = X + row * a.ldx;
-      float ss = 0.f;
-      for (int64_t c = (int64_t)lane * 8; c < K; c += 64 * 8) {
-        float v[8];
-        load8(xp + c, v);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
-      }
-      ss = wave_sum(ss);
-      if (lane == 0) s_inv[row] = rsqrtf(ss / (float)K + a.eps);
-    }
-    __syncthreads();
-  }
+  // input rows (<= 16) as A fragments for all K (K = 256 KC): step u covers
+  // k = 32u + 8g, so lanes r, r+16, r+32, r+48 hold all of row r and the
+  // row statistics need no loads of their own. The input loads go out
+  // together with the ring's first DMA (one memory round trip for both; a
+  // separate statistics pass and a barrier would cost two more), the norm
+  // weight (2 KB, shared by every block) once the statistics are known.
   const bool xok = r < a.NB;
   const T *xr = X + (xok ? r : 0) * a.ldx;
   V8 xa[KC * 8];
 #pragma unroll
-  for (int u = 0; u < KC * 8; ++u) {
-    const int64_t c = (int64_t)u * 32 + g * 8;
-    const bool ok = c < K && xok;
-    xa[u] = ld16(xr + c, ok);
-    if constexpr (NORM) {
-      // zero where !ok: both factors are zero there
-      const V8 nw8 = ld16((const T *)a.norm_w + c, ok);
-      const float inv = s_inv[r];
+  for (int u = 0; u < KC * 8; ++u) xa[u] = ld16(xr + (int64_t)u * 32 + g * 8, xok);
+  __builtin_amdgcn_sched_barrier(0); // all of them out before the first use
+  if constexpr (NORM) {
+    float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xa[u][i] = from_f32<T>((to_f32(xa[u][i]) * inv) * to_f32(nw8[i]));
+    for (int u = 0; u < KC * 8; ++u)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = to_f32(xa[u][i]);
+        ss += v * v;
+      }
+    ss += __shfl_xor(ss, 16, kWave);
+    ss += __shfl_xor(ss, 32, kWave);
+    const float inv = rsqrtf(ss / (float)K + a.eps);
+    // 8 steps' norm weights per batch of loads: one (L2) round trip per
+    // batch, at 32 extra registers
+#pragma unroll
+    for (int u0 = 0; u0 < KC * 8; u0 += 8) {
+      V8 nw8[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) nw8[u] = ld16((const T *)a.norm_w + (int64_t)(u0 + u) * 32 + g * 8, true);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          xa[u0 + u][i] = from_f32<T>((to_f32(xa[u0 + u][i]) * inv) * to_f32(nw8[u][i]));
     }
   }
 
