@@ -128,8 +128,12 @@ struct GemvArgs {
 // wave w covers K slice w of every tile.
 constexpr int kGemvMaxBlocks = 1024;
 
-template <typename T, int EPI, int ACT, bool NORM, int MAXW>
+// RT = weight rows per tile: 16, or 8 for launches with few tiles (the
+// MFMA's columns 8..15 then repeat rows 0..7 from LDS and are discarded), so
+// twice as many CUs each fetch half the bytes.
+template <typename T, int EPI, int ACT, bool NORM, int MAXW, int RT = 16>
 __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t tiles) {
+  static_assert(RT == 16 || (RT == 8 && EPI != kEpiSwiGLU), "tile rows");
   typedef typename VecT<T>::v8 V8;
   constexpr int NS = kGemvWaveK / 32; // MFMA steps per wave batch
   __shared__ f32x4 red[EPI == kEpiSwiGLU ? 2 : 1][MAXW][64];
@@ -137,6 +141,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   __shared__ float s_part[MAXW][16];
   const int lane = lane_id(), w = wave_id(), nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
+  const int rr = r % RT; // this lane's weight row in the tile
   const int64_t N = a.N, K = a.K;
   const T *X = (const T *)a.x;
   const T *W = (const T *)a.W;
@@ -150,7 +155,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       row0 = (tile >> 1) * 64 + (tile & 1) * 16;
       row1 = row0 + 32;
     } else {
-      row0 = tile * 16;
+      row0 = tile * RT;
       row1 = 0;
     }
   };
@@ -159,8 +164,8 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   auto load_w = [&](int64_t tile, int64_t k, V8 (&b0)[NS], V8 (&b1)[NS], T (&res)[4]) {
     int64_t row0, row1;
     rows_of(tile, row0, row1);
-    const bool w0ok = row0 + r < N;
-    const T *w0 = W + (w0ok ? row0 + r : 0) * K;
+    const bool w0ok = row0 + rr < N;
+    const T *w0 = W + (w0ok ? row0 + rr : 0) * K;
     const bool w1ok = (EPI == kEpiSwiGLU) && (row1 + r < N);
     const T *w1 = W + (w1ok ? row1 + r : 0) * K;
 #pragma unroll
@@ -176,7 +181,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int b = 4 * g + i;
-        res[i] = ld1(rs + (int64_t)b * a.ldy + row0 + r, row0 + r < N && b < a.NB);
+        res[i] = ld1(rs + (int64_t)b * a.ldy + row0 + rr, row0 + rr < N && b < a.NB);
       }
     }
   };
@@ -194,7 +199,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
   // (row statistics, normalisation) while the weights are still on the way.
   constexpr int NSET = EPI == kEpiSwiGLU ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) char gemv_smem[];
-  V8 *wslot = reinterpret_cast<V8 *>(gemv_smem) + (size_t)w * NSET * (16 * 32);
+  V8 *wslot = reinterpret_cast<V8 *>(gemv_smem) + (size_t)w * NSET * (RT * 32);
   const int drow = lane >> 5, dpos = lane & 31;
   auto issue_w = [&](int64_t tile, T (&res)[4]) {
     int64_t row0, row1;
@@ -203,14 +208,14 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
     for (int set = 0; set < NSET; ++set) {
       const int64_t rb = set == 0 ? row0 : row1;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < RT / 2; ++j) {
         const int row = 2 * j + drow;
         const int64_t gr = rb + row < N ? rb + row : N - 1;
         int64_t kk = k_begin + (int64_t)((dpos ^ row) * 8);
         kk = kk < K - 8 ? kk : K - 8;
         __builtin_amdgcn_global_load_lds(
             (const void *)(W + gr * K + kk),
-            (__attribute__((address_space(3))) void *)(wslot + set * (16 * 32) + j * 64), 16, 0, 0);
+            (__attribute__((address_space(3))) void *)(wslot + set * (RT * 32) + j * 64), 16, 0, 0);
       }
     }
     if constexpr (EPI == kEpiResidual) {
@@ -219,7 +224,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int b = 4 * g + i;
-        res[i] = ld1(rs + (int64_t)b * a.ldy + row0 + r, row0 + r < N && b < a.NB);
+        res[i] = ld1(rs + (int64_t)b * a.ldy + row0 + rr, row0 + rr < N && b < a.NB);
       }
     }
   };
@@ -229,7 +234,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
     __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8)); // vmcnt(0)
 #pragma unroll
     for (int u = 0; u < NS; ++u) {
-      b0[u] = wslot[r * 32 + ((u * 4 + g) ^ r)];
+      b0[u] = wslot[rr * 32 + ((u * 4 + g) ^ rr)];
       if constexpr (EPI == kEpiSwiGLU) b1[u] = wslot[16 * 32 + r * 32 + ((u * 4 + g) ^ r)];
     }
     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): reads done
@@ -278,7 +283,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       // flight: the input loads are asm, since after an LDS-DMA the
       // compiler's own wait for a plain load is vmcnt(0)
       __builtin_amdgcn_sched_barrier(0);
-      vm_wait_tied<8 * NSET + (EPI == kEpiResidual ? 4 : 0)>(xa, nwv);
+      vm_wait_tied<(RT / 2) * NSET + (EPI == kEpiResidual ? 4 : 0)>(xa, nwv);
       float ss = 0.f;
 #pragma unroll
       for (int u = 0; u < NS; ++u)
@@ -340,7 +345,8 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
         for (int i = 1; i < nw; ++i) acc1 += red[1][i][lane];
       }
       // D layout of 16x16x32: lane -> column r (weight row), rows b = 4g + i.
-      const int64_t n0 = row0 + r, n1 = row1 + r;
+      // (RT = 8: columns 8..15 repeat rows 0..7 and are not stored)
+      const int64_t n0 = r < RT ? row0 + r : INT64_MAX, n1 = row1 + r;
       T *Y = (T *)a.y;
       if (a.am_val) { // running argmax over this block's columns
 #pragma unroll
@@ -719,7 +725,11 @@ static int launch_gemv(GemvArgs a, hipStream_t st, const char *name) {
     gemv_scalar_kernel<T, EPI, ACT, NORM><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a, NO);
     return check_launch(name);
   }
-  const int64_t tiles = (EPI == kEpiSwiGLU) ? (a.N / 64) * 2 : (a.N + 15) / 16;
+  // 8-row tiles when 16-row ones would leave most CUs idle (not for SwiGLU,
+  // whose tiles pair gate and up rows, nor with argmax partials, whose
+  // workspace is sized for 16-row tiles)
+  const bool rt8 = EPI != kEpiSwiGLU && !a.am_val && (a.N + 15) / 16 < 128;
+  const int64_t tiles = (EPI == kEpiSwiGLU) ? (a.N / 64) * 2 : rt8 ? (a.N + 7) / 8 : (a.N + 15) / 16;
   if (tiles > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: N too large", name);
   if constexpr (EPI == kEpiPlain) {
     if (launch_wide<T, NORM>(a, st)) return check_launch(name);
@@ -734,7 +744,14 @@ static int launch_gemv(GemvArgs a, hipStream_t st, const char *name) {
   const int64_t blocks = tiles < kGemvMaxBlocks ? tiles : kGemvMaxBlocks;
   // LDS weight slots of the one-batch-per-wave path (16 rows x 512 bytes per
   // row set and wave)
-  const size_t lds = (size_t)nw * (EPI == kEpiSwiGLU ? 2 : 1) * 16 * 512;
+  const size_t lds = (size_t)nw * (EPI == kEpiSwiGLU ? 2 : 1) * (rt8 ? 8 : 16) * 512;
+  if constexpr (EPI != kEpiSwiGLU) {
+    if (rt8) {
+      gemv16_kernel<T, EPI, ACT, NORM, MAXW, 8>
+          <<<dim3((unsigned)blocks), dim3((unsigned)(nw * 64)), lds, st>>>(a, tiles);
+      return check_launch(name);
+    }
+  }
   gemv16_kernel<T, EPI, ACT, NORM, MAXW>
       <<<dim3((unsigned)blocks), dim3((unsigned)(nw * 64)), lds, st>>>(a, tiles);
   return check_launch(name);
