@@ -93,11 +93,13 @@ def test_linear_module_3d_input(dev):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("bsz", [1, 8, 16])
-@pytest.mark.parametrize("n,k", [(3072, 1024), (1024, 3072), (4096, 1024), (1000, 200), (24, 2048)])
+@pytest.mark.parametrize("n,k", [(3072, 1024), (1024, 3072), (4096, 1024), (1000, 200), (24, 2048),
+                                 (1003, 4096)])
 def test_gemv_parity(dev, dtype, bsz, n, k):
     """[1x1024]@[1024x3072] and [1x3072]@[3072x1024]; plus the
     decode-step shapes at batch 8/16 and ragged sizes (a last row tile past N,
-    K shorter than one 256-wide wave batch)."""
+    K shorter than one 256-wide wave batch, K longer than 12 wave batches with
+    8-row tiles)."""
     x, w, _ = _mk(bsz, n, k, dtype, seed=5)
     y = ext().gemv(x.to(dev), w.to(dev))
     close(y, oracle.gemv(x, w), what=f"gemv b{bsz} {n}x{k}")
@@ -148,7 +150,7 @@ def test_gemv_fused_input_rmsnorm(dev, bsz, n, k):
     close(y, oracle.linear_act(oracle.rmsnorm(x, nw, 1e-6), w), what="gemv(rmsnorm(x))")
 
 
-@pytest.mark.parametrize("n,k", [(1024, 2048), (1024, 3072)])
+@pytest.mark.parametrize("n,k", [(1024, 2048), (1024, 3072), (1003, 1000)])
 def test_gemv_fused_residual_add(dev, n, k):
     x, w, _ = _mk(8, n, k, torch.bfloat16, seed=11)
     r = torch.randn(8, n, generator=torch.Generator().manual_seed(12)).bfloat16()
