@@ -21,12 +21,16 @@ def _qkv(b, sq, sk, hq, hkv, d, dtype, seed=0):
 @pytest.mark.parametrize("window", [(-1, -1), (511, 0)])
 def test_prefill_baseline_config(dev, window):
     """B4 S2048 16/8 heads D128 causal (+ window 512).
-    Full-size run; the oracle checks batch 3, KV head 5 (query heads 10, 11)."""
+    Every output row is checked: the oracle runs per (batch, KV head) pair
+    (its 2 query heads), all 32 pairs."""
     q, k, v = _qkv(4, 2048, 2048, 16, 8, 128, torch.bfloat16)
-    o = flash_attn_func(q.to(dev), k.to(dev), v.to(dev), causal=True, window_size=window)
-    e = oracle.attention(q[3:4, :, 10:12], k[3:4, :, 5:6], v[3:4, :, 5:6], causal=True, window=window)
-    close(o[3:4, :, 10:12], e, what=f"prefill window={window}")
-    assert torch.isfinite(o.float()).all()
+    o = flash_attn_func(q.to(dev), k.to(dev), v.to(dev), causal=True, window_size=window).cpu()
+    for b in range(4):
+        for hk in range(8):
+            e = oracle.attention(q[b:b + 1, :, 2 * hk:2 * hk + 2], k[b:b + 1, :, hk:hk + 1],
+                                 v[b:b + 1, :, hk:hk + 1], causal=True, window=window)
+            close(o[b:b + 1, :, 2 * hk:2 * hk + 2], e,
+                  what=f"prefill window={window} batch {b} kv head {hk}")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -78,7 +82,8 @@ def test_prefill_uniform_v_special_case(dev):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_decode_baseline_config(dev, dtype):
-    """B32, 16/8 heads, D128, cache length 4096."""
+    """B32, 16/8 heads, D128, cache length 4096; all 32
+    sequences against the oracle."""
     g = torch.Generator().manual_seed(6)
     B, Hq, Hkv, D, L = 32, 16, 8, 128, 4096
     q = torch.randn(B, 1, Hq, D, generator=g).to(dtype)
@@ -86,9 +91,8 @@ def test_decode_baseline_config(dev, dtype):
     vc = torch.randn(B, Hkv, L, D, generator=g).to(dtype)
     lens = torch.full((B,), L, dtype=torch.int32)
     o = decode_attention(q.to(dev), kc.to(dev), vc.to(dev), lens.to(dev))
-    sel = [0, 17, 31]
-    e = oracle.decode_attention(q[sel], kc[sel], vc[sel], lens[sel].tolist())
-    close(o[sel], e, what="decode")
+    e = oracle.decode_attention(q, kc, vc, lens.tolist())
+    close(o, e, what="decode")
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (8, 1, 128), (4, 4, 64), (6, 2, 128)])
@@ -190,5 +194,21 @@ def test_decode_fused_prologue_matches_unfused(dev, hq, hkv, norm):
     got = C.attn_decode_fused(qkv, qw, kw, cos, sin, 1e-6, kc, vc, pos + 1)
     assert torch.equal(kc, kc2) and torch.equal(vc, vc2), "cache append differs"
     close(got, ref, atol=1e-2, rtol=1e-2, what="fused decode")
-    e = oracle.decode_attention(q.cpu(), kc2.cpu(), vc2.cpu(), (pos + 1).tolist())
+    # independent of the HIP prologue: q and the appended K/V from the oracle
+    # (QK-RMSNorm over D, RoPE at position pos[b], torchpp/attention/gqa.py:90-116)
+    x = qkv.cpu().view(B, hq + 2 * hkv, D)
+    qh, kh, vh = x[:, :hq], x[:, hq:hq + hkv], x[:, hq + hkv:]
+    if norm:
+        qh, kh = oracle.rmsnorm(qh, qw.cpu(), 1e-6), oracle.rmsnorm(kh, kw.cpu(), 1e-6)
+    pl = pos.cpu().long()
+    cr, sr = cos.cpu()[pl][:, None], sin.cpu()[pl][:, None]  # [B, 1, D]
+    qh, kh = oracle.rope(qh[:, :, None], cr[:, :, None], sr[:, :, None])[:, :, 0], \
+        oracle.rope(kh[:, :, None], cr[:, :, None], sr[:, :, None])[:, :, 0]
+    k_ref, v_ref = kc2.cpu().clone(), vc2.cpu().clone()
+    for b in range(B):
+        k_ref[b, :, pl[b]] = kh[b]
+        v_ref[b, :, pl[b]] = vh[b]
+    close(kc.cpu(), k_ref, what="fused decode: appended K vs oracle")
+    assert torch.equal(vc.cpu(), v_ref), "fused decode: appended V differs from the projection"
+    e = oracle.decode_attention(qh[:, None], k_ref, v_ref, (pos + 1).tolist())
     close(got, e, what="fused decode vs oracle")

@@ -92,3 +92,59 @@ def test_graph_replays_are_stable(dev):
         got = m.generate_greedy(ids, 8, use_graph=True)
         torch.cuda.synchronize()
         assert torch.equal(got, want)
+
+
+@torch.inference_mode()
+def test_generate_with_decreasing_batch_reuses_caches(dev):
+    """generate()/generate_greedy() at batch 3 then at batch 2 (caches
+    allocated for 3 are reused through [:2] views) gives the tokens of a
+    fresh run at batch 2."""
+    ids = torch.randint(0, TINY.vocab_size, (3, 14), generator=torch.Generator().manual_seed(8)).to(dev)
+    fresh = _model(dev, seed=9)
+    want = fresh.generate_greedy(ids[:2], 6, use_graph=False)
+    want_ref = fresh.generate(ids[:2], max_new_token=6, sampling_strategy="greedy")
+    m = _model(dev, seed=9)
+    m.generate_greedy(ids, 6, use_graph=True)
+    assert torch.equal(m.generate_greedy(ids[:2], 6, use_graph=True), want)
+    m.generate(ids, max_new_token=6, sampling_strategy="greedy")
+    assert torch.equal(m.generate(ids[:2], max_new_token=6, sampling_strategy="greedy"), want_ref)
+
+
+@torch.inference_mode()
+def test_graph_replay_after_decode_workspace_grew(dev):
+    """A decode graph captured before an eager decode call that needs a larger
+    workspace than the binding holds keeps working: the old workspace stays
+    alive for the graph (its counters untouched by the larger call)."""
+    import ctypes
+
+    from torchplusplus_amd._native import lib
+    from torchplusplus_amd.attention import decode_attention
+
+    m = _model(dev, seed=10)
+    B, S, N = 2, 11, 6
+    ids = torch.randint(0, TINY.vocab_size, (B, S), generator=torch.Generator().manual_seed(11)).to(dev)
+    m.setup_kv_cache(S + N, B)
+    m.reset_kv_cache()
+    logits = m.forward_impl(ids, m.kv_cache_array, 0, last_only=True)
+    first = logits[:, -1].float().argmax(-1)
+    dec = GreedyDecoder(m, B)
+    a = dec.run(first, S, N, use_graph=True)
+    # an eager decode whose workspace exceeds the binding's initial 4 MiB
+    Bb, Hq, Hkv, D, L = 125, 32, 4, 128, 256
+    f = lib().tpp_attn_decode_workspace_size
+    f.restype = ctypes.c_size_t
+    need = f(*(ctypes.c_int64(v) for v in (Bb, Hq, Hkv, D, L)))
+    assert need > 4 * 1024 * 1024, need
+    g = torch.Generator(device=dev).manual_seed(12)
+    q = torch.randn(Bb, 1, Hq, D, device=dev, generator=g).bfloat16()
+    kc = torch.randn(Bb, Hkv, L, D, device=dev, generator=g).bfloat16()
+    vc = torch.randn(Bb, Hkv, L, D, device=dev, generator=g).bfloat16()
+    decode_attention(q, kc, vc)
+    del q, kc, vc
+    torch.cuda.synchronize()
+    # allocate over freed memory, then replay the old graph
+    junk = torch.full((8 << 20,), 7.0, device=dev)
+    b = dec.run(first, S, N, use_graph=True)
+    torch.cuda.synchronize()
+    del junk
+    assert torch.equal(a, b)

@@ -18,7 +18,7 @@ import torch
 import torch.nn as nn
 
 from torchplusplus_amd._native import ext as _ext
-from torchplusplus_amd.attention.flash import decode_attention, flash_attn_func
+from torchplusplus_amd.attention.flash import flash_attn_func
 from torchplusplus_amd.dlops.linear import linear
 from torchplusplus_amd.llmops.kvcache import KVCache
 
@@ -92,23 +92,21 @@ class GroupedQueryAttention(nn.Module):
             start = kv_cache.cache_len if cache_pos is None else int(cache_pos)
             kv_cache.ensure(bs, start + seq_len)
             total = start + seq_len
-            if seq_len == 1 and kv_cache.k_cache.shape[0] == bs:
+            # the cache may hold more sequences than this call (allocated for
+            # an earlier, larger batch): the kernels get this batch's rows
+            kc_b, vc_b = kv_cache.k_cache[:bs], kv_cache.v_cache[:bs]
+            if seq_len == 1:
                 # one new token: QK-norm + RoPE + cache append fused into the
                 # split-KV decode kernel
                 seqlens = torch.full((bs,), total, dtype=torch.int32, device=dev)
                 kv_cache.cache_len = max(kv_cache.cache_len, total)
-                return self.decode_fused(qkv, cos, sin, kv_cache.k_cache, kv_cache.v_cache,
+                return self.decode_fused(qkv, cos, sin, kc_b, vc_b,
                                          seqlens).reshape(bs, seq_len, self.d_out)
             positions = torch.full((bs,), start, dtype=torch.int32, device=dev)
-            q = self.rope_cache(qkv, cos, sin, kv_cache.k_cache, kv_cache.v_cache, positions)
+            q = self.rope_cache(qkv, cos, sin, kc_b, vc_b, positions)
             kv_cache.cache_len = max(kv_cache.cache_len, start + seq_len)
-            if seq_len == 1:
-                seqlens = torch.full((bs,), total, dtype=torch.int32, device=dev)
-                o = decode_attention(q, kv_cache.k_cache, kv_cache.v_cache, seqlens)
-            else:
-                kc = kv_cache.k_cache[:bs, :, :total].transpose(1, 2)
-                vc = kv_cache.v_cache[:bs, :, :total].transpose(1, 2)
-                o = flash_attn_func(q, kc, vc, causal=True)
+            o = flash_attn_func(q, kc_b[:, :, :total].transpose(1, 2),
+                                vc_b[:, :, :total].transpose(1, 2), causal=True)
         else:
             k = torch.empty(bs, self.n_kv_heads, seq_len, self.head_dim, dtype=qkv.dtype, device=dev)
             v = torch.empty_like(k)

@@ -35,6 +35,9 @@
 // waves (LDS) and chunks (a small merge kernel per (batch, KV head)).
 #include "tpp_common.hpp"
 
+#include <atomic>
+#include <mutex>
+
 namespace tpp {
 
 struct AttnArgs {
@@ -1073,6 +1076,21 @@ struct DecodePlan {
   size_t o_bytes, ml_bytes, ws_bytes;
 };
 
+// Partial-slot layout of a split plan: in-kernel merge (one padded slot per
+// split) or merge kernel (D outputs, then m/l pairs; the counter region stays
+// reserved and untouched, so a workspace shared with in-kernel-merge calls
+// keeps its counters at zero).
+static void use_merge_layout(DecodePlan &pl, size_t slots, int64_t D, bool inline_merge) {
+  pl.inline_merge = inline_merge;
+  if (inline_merge) {
+    pl.o_bytes = slots * (size_t)(D + 32) * sizeof(float);
+    pl.ml_bytes = 0;
+  } else {
+    pl.o_bytes = slots * (size_t)D * sizeof(float);
+    pl.ml_bytes = slots * 2 * sizeof(float);
+  }
+}
+
 // Split-KV plan: about one 8-wave block per CU, each (batch, KV head) pair's
 // keys split into whole load batches; one split needs no merge kernel.
 static DecodePlan plan_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t Lmax) {
@@ -1096,21 +1114,70 @@ static DecodePlan plan_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
   if (pl.nsplit == 1) {
     pl.o_bytes = pl.ml_bytes = 0;
     pl.ws_bytes = 16;
-  } else if (pl.inline_merge) {
-    // one arrival counter per (batch, KV head) pair in a fixed region at the
-    // start (calls of every shape and mode keep partials out of it), then
-    // slots of D partial outputs + m + l padded to whole 128-byte lines
-    pl.o_bytes = slots * (size_t)(D + 32) * sizeof(float);
-    pl.ml_bytes = 0;
-    pl.ws_bytes = kDecCounterBytes + pl.o_bytes;
   } else {
-    // the counter region stays reserved (and untouched) here too, so a
-    // workspace shared with inline-merge calls keeps its counters at zero
-    pl.o_bytes = slots * (size_t)D * sizeof(float);
-    pl.ml_bytes = slots * 2 * sizeof(float);
-    pl.ws_bytes = kDecCounterBytes + pl.o_bytes + pl.ml_bytes;
+    // The size is the in-kernel merge layout's whatever the mode, so a call
+    // that falls back to the merge kernel (placement check below) fits too.
+    // One arrival counter per (batch, KV head) pair in a fixed region at the
+    // start (calls of every shape and mode keep partials out of it), then
+    // slots of D partial outputs + m + l padded to whole 128-byte lines.
+    pl.ws_bytes = kDecCounterBytes + slots * (size_t)(D + 32) * sizeof(float);
+    use_merge_layout(pl, slots, D, pl.inline_merge);
   }
   return pl;
+}
+
+// ---- placement check for the in-kernel split merge -------------------------
+// The in-kernel merge relies on workgroups with equal blockIdx % 8 running on
+// one XCD (so their partials and the arrival counter meet in one L2). Once
+// per device a probe launch records HW_REG_XCC_ID for 512 workgroups; if any
+// workgroup's XCD differs from that of workgroup (id % 8), decode falls back
+// to the merge kernel on that device. The probe needs a synchronous read
+// back, so it is skipped (merge kernel for that call, no verdict cached)
+// while the caller's stream is being captured.
+constexpr int kXcdProbeBlocks = 512;
+static __device__ int g_xcd_probe[kXcdProbeBlocks];
+static std::atomic<int> g_xcd_state[64]; // 0 unknown, 1 holds, 2 does not hold
+static std::mutex g_xcd_mu;
+
+__global__ __launch_bounds__(64) void xcd_probe_kernel(int *__restrict__ out) {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  if (threadIdx.x == 0) out[blockIdx.x] = (int)(v & 0xfu);
+}
+
+static bool xcd_grouping_holds(hipStream_t st) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return false;
+  }
+  int s = g_xcd_state[dev].load(std::memory_order_acquire);
+  if (s) return s == 1;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return false;
+  }
+  std::lock_guard<std::mutex> lock(g_xcd_mu);
+  s = g_xcd_state[dev].load(std::memory_order_acquire);
+  if (s) return s == 1;
+  int *d = nullptr;
+  int h[kXcdProbeBlocks];
+  hipError_t e = hipGetSymbolAddress((void **)&d, HIP_SYMBOL(g_xcd_probe));
+  if (e == hipSuccess) {
+    xcd_probe_kernel<<<dim3(kXcdProbeBlocks), dim3(64), 0, st>>>(d);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  bool ok = true;
+  for (int i = 0; i < kXcdProbeBlocks; ++i) ok = ok && h[i] == h[i % 8];
+  g_xcd_state[dev].store(ok ? 1 : 2, std::memory_order_release);
+  return ok;
 }
 
 template <typename T, int D, int G>
@@ -1220,14 +1287,16 @@ static int decode_impl(const char *name, AttnArgs &a, int64_t D, int64_t Lmax,
     return set_error(TPP_E_UNSUPPORTED, "%s: more than %d query heads per KV head", name,
                      kDecMaxG);
   if (!strides16(a)) return set_error(TPP_E_INVALID, "%s: 16-byte alignment required", name);
-  const DecodePlan pl = plan_decode(a.B, a.Hq, a.Hkv, D, Lmax);
+  DecodePlan pl = plan_decode(a.B, a.Hq, a.Hkv, D, Lmax);
   if (!workspace || ws_bytes < pl.ws_bytes || (uintptr_t)workspace % 128 != 0)
     return set_error(TPP_E_WORKSPACE, "%s: 128-byte aligned workspace of %zu bytes required",
                      name, pl.ws_bytes);
+  hipStream_t st = as_stream(stream);
+  if (pl.inline_merge && !xcd_grouping_holds(st))
+    use_merge_layout(pl, (size_t)a.B * a.Hq * pl.nsplit, D, false);
   int *counters = pl.inline_merge ? (int *)workspace : nullptr;
   float *ws_o = (float *)((char *)workspace + kDecCounterBytes);
   float *ws_ml = (float *)((char *)ws_o + pl.o_bytes);
-  hipStream_t st = as_stream(stream);
   const dim3 grid = pl.inline_merge
                         ? dim3((unsigned)(pl.nsplit * a.Hkv * a.B))
                         : dim3((unsigned)pl.nsplit, (unsigned)a.Hkv, (unsigned)a.B);
@@ -1275,6 +1344,9 @@ extern "C" int tpp_attn_decode_fused(const void *qkv, const void *q_norm_w, cons
   if (cs_dtype != TPP_F16 && cs_dtype != TPP_BF16 && cs_dtype != TPP_F32)
     return set_error(TPP_E_UNSUPPORTED, "%s: cos/sin dtype", name);
   if (ctx <= 0 || ctx > 0x7fffffff) return set_error(TPP_E_INVALID, "%s: ctx", name);
+  if (ctx < Lmax) // every cache position must have a table row (no clamping)
+    return set_error(TPP_E_INVALID, "%s: cos/sin hold %lld positions, fewer than the cache length %lld",
+                     name, (long long)ctx, (long long)Lmax);
   if (B > 0xffff || Hkv > 0xffff || Lmax > 0x7fffffff)
     return set_error(TPP_E_UNSUPPORTED, "%s: dimension too large", name);
   const int64_t qs[3] = {0, 0, 0};

@@ -254,6 +254,8 @@ void qkv_rope_cache(at::Tensor qkv, at::Tensor q_out, at::Tensor k_cache, at::Te
                   cos.size(1) == D && sin.sizes() == cos.sizes() &&
                   sin.scalar_type() == cos.scalar_type(),
               "cos/sin must be contiguous [ctx, D] tables");
+  TORCH_CHECK(cos.size(0) >= Lmax, "cos/sin hold ", cos.size(0),
+              " positions, fewer than the cache length ", Lmax);
   const void *qw = nullptr, *kw = nullptr;
   if (q_norm_w.has_value() && q_norm_w->defined()) {
     TORCH_CHECK(q_norm_w->numel() == D && q_norm_w->scalar_type() == qkv.scalar_type() &&
@@ -431,15 +433,21 @@ std::vector<at::Tensor> gemv_argmax(at::Tensor input, at::Tensor weight,
 // ---- attention (flash_attn_func contract) ----------------------------------
 // Zero-filled per-device scratch, allocated once and reused, so a captured
 // decode graph keeps one stable pointer (intentionally leaked: no tensor
-// destructor runs after the caching allocator is torn down at exit). Slot 1
-// belongs to decode attention alone: its arrival counters must stay zero
-// between calls, which the kernel guarantees but another user of the same
-// bytes would not. Calls that share a slot must not overlap, so a call on a
-// stream other than the slot's last one first makes its stream wait for that
-// stream (an event); while a stream is being captured the capture is ordered
-// after earlier work by the caller (torch.cuda.graph synchronizes first).
+// destructor runs after the caching allocator is torn down at exit). When a
+// call needs more than the slot holds, a larger buffer replaces it for later
+// calls, and the old one is kept alive (`retired`) until the process ends:
+// a graph captured earlier still holds its address in its kernel arguments
+// and keeps using it (its counters stay zero, since only that graph's calls
+// touch it). Slot 1 belongs to decode attention alone: its arrival counters
+// must stay zero between calls, which the kernel guarantees but another user
+// of the same bytes would not. Calls that share a slot must not overlap, so a
+// call on a stream other than the slot's last one first makes its stream
+// wait for that stream (an event); while a stream is being captured the
+// capture is ordered after earlier work by the caller (torch.cuda.graph
+// synchronizes first).
 struct ScratchSlot {
   at::Tensor t;
+  std::vector<at::Tensor> retired;
   hipStream_t last = nullptr;
   hipEvent_t ev = nullptr;
 };
@@ -461,6 +469,7 @@ at::Tensor cached_workspace(const at::Tensor &like, size_t bytes, int slot = 0) 
   if (!e.t.defined() || (size_t)e.t.numel() * 4 < bytes) {
     int64_t n = (int64_t)((bytes + 3) / 4);
     n = n < (1 << 20) ? (1 << 20) : n;
+    if (e.t.defined()) e.retired.push_back(e.t);
     e.t = torch::zeros({n}, like.options().dtype(at::kFloat));
   }
   e.last = capturing ? nullptr : s;
@@ -621,6 +630,8 @@ at::Tensor attn_decode_fused(at::Tensor qkv, c10::optional<at::Tensor> q_norm_w,
                   sin.sizes() == cos.sizes() && sin.scalar_type() == cos.scalar_type() &&
                   dtype_code(cos) >= 0,
               "cos/sin must be contiguous [ctx, D] tables");
+  TORCH_CHECK(cos.size(0) >= Lmax, "cos/sin hold ", cos.size(0),
+              " positions, fewer than the cache length ", Lmax);
   const void *qw = norm_ptr(q_norm_w, qkv, D), *kw = norm_ptr(k_norm_w, qkv, D);
   c10::DeviceGuard g(qkv.device());
   auto o = torch::empty({B, 1, Hq, D}, qkv.options());

@@ -282,6 +282,9 @@ extern "C" int tpp_qkv_rope_cache(const void *qkv, void *q_out, void *k_cache,
     return set_error(TPP_E_INVALID, "%s: null pointer argument", name);
   if (B <= 0 || S <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || Lmax <= 0 || ctx <= 0)
     return set_error(TPP_E_INVALID, "%s: invalid shapes", name);
+  if (ctx < Lmax) // every cache position must have a table row (no clamping)
+    return set_error(TPP_E_INVALID, "%s: cos/sin hold %lld positions, fewer than the cache length %lld",
+                     name, (long long)ctx, (long long)Lmax);
   if (D != 64 && D != 128 && D != 256)
     return set_error(TPP_E_UNSUPPORTED, "%s: head_dim %lld not in {64,128,256}", name,
                      (long long)D);

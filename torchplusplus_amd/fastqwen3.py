@@ -220,7 +220,7 @@ class GreedyDecoder:
         m, B, resid = self.m, self.B, self.resid
         for i, blk in enumerate(m.transformer_blocs):
             at, n1, n2 = blk.attn, blk.rms_norm1, blk.rms_norm2
-            kc, vc = self.caches[i].k_cache, self.caches[i].v_cache
+            kc, vc = self.caches[i].k_cache[:B], self.caches[i].v_cache[:B]
             qkv = _C.gemv_fused(resid, at.fused_qkv_weight(), n1.weight, n1.eps)
             o = at.decode_fused(qkv, m.cos, m.sin, kc, vc, self.seqlens)
             _C.gemv_fused(o.view(B, 1, at.d_out), at.out_projection.weight, None, 1e-6, resid)
