@@ -237,6 +237,26 @@ int tpp_attn_decode(const void *q, const void *k_cache, const void *v_cache,
                     int window_left, int dtype, void *workspace,
                     size_t ws_bytes, void *stream);
 
+/* tpp_attn_decode without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * kernels run on a 4 MiB static device array held by each GPU the library
+ * runs on until the process ends; shapes whose split plan needs more than
+ * that (tpp_attn_decode_workspace_size > 4 MiB) are rejected with
+ * TPP_E_UNSUPPORTED. The first call on a device sets the array up (with that
+ * device current) and queues a small fill kernel on `stream`. All calls on
+ * one GPU share the array: calls that overlap on one GPU (e.g. on two
+ * streams without ordering) race. Never calls hipMalloc/hipFree. Arguments
+ * and results as tpp_attn_decode. */
+int tpp_attn_decode_noalloc(const void *q, const void *k_cache,
+                            const void *v_cache, void *o,
+                            const int64_t *q_strides, const int64_t *k_strides,
+                            const int64_t *v_strides, const int64_t *o_strides,
+                            const int32_t *seqlens, int64_t B, int64_t Hq,
+                            int64_t Hkv, int64_t D, int64_t Lmax,
+                            float softmax_scale, int window_left, int dtype,
+                            void *stream);
+
 /* Decode attention with the per-layer prologue fused in (replaces
  * tpp_qkv_rope_cache + tpp_attn_decode for one new token per sequence): the
  * new token's raw projection qkv [B, (Hq + 2*Hkv) * D] is split into heads,

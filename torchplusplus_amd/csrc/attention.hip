@@ -1145,14 +1145,14 @@ __global__ __launch_bounds__(64) void xcd_probe_kernel(int *__restrict__ out) {
   if (threadIdx.x == 0) out[blockIdx.x] = (int)(v & 0xfu);
 }
 
-static bool xcd_grouping_holds(hipStream_t st) {
+static bool xcd_grouping_holds(hipStream_t st, bool may_probe) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
     (void)hipGetLastError();
     return false;
   }
   int s = g_xcd_state[dev].load(std::memory_order_acquire);
-  if (s) return s == 1;
+  if (s || !may_probe) return s == 1;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
     (void)hipGetLastError();
@@ -1276,7 +1276,7 @@ extern "C" size_t tpp_attn_decode_workspace_size(int64_t B, int64_t Hq, int64_t 
 
 static int decode_impl(const char *name, AttnArgs &a, int64_t D, int64_t Lmax,
                        const int32_t *seqlens, const DecodeFuse &fz, int dtype, void *workspace,
-                       size_t ws_bytes, void *stream) {
+                       size_t ws_bytes, void *stream, bool may_probe = true) {
   if (int e = check_attn(name, a, D)) return e;
   if (a.B == 0) return TPP_OK;
   // the kernel reads cache row 0 even for empty sequences (clamped loads)
@@ -1292,7 +1292,7 @@ static int decode_impl(const char *name, AttnArgs &a, int64_t D, int64_t Lmax,
     return set_error(TPP_E_WORKSPACE, "%s: 128-byte aligned workspace of %zu bytes required",
                      name, pl.ws_bytes);
   hipStream_t st = as_stream(stream);
-  if (pl.inline_merge && !xcd_grouping_holds(st))
+  if (pl.inline_merge && !xcd_grouping_holds(st, may_probe))
     use_merge_layout(pl, (size_t)a.B * a.Hq * pl.nsplit, D, false);
   int *counters = pl.inline_merge ? (int *)workspace : nullptr;
   float *ws_o = (float *)((char *)workspace + kDecCounterBytes);
@@ -1323,6 +1323,82 @@ extern "C" int tpp_attn_decode(const void *q, const void *k_cache, const void *v
                          0);
   DecodeFuse fz{};
   return decode_impl(name, a, D, Lmax, seqlens, fz, dtype, workspace, ws_bytes, stream);
+}
+
+// ---- allocation-free decode ------------------------------------------------
+// tpp_attn_decode_noalloc runs the decode kernels on a file-scope device
+// array instead of a caller workspace, for callers that cannot allocate. Each
+// device holds its own copy of `scratch`; its address on a device comes from
+// hipGetSymbolAddress at the first call with that device current (the host
+// symbol itself is not a device address) and is kept per device. The first
+// call also zeroes the arrival-counter region with a fill kernel on the
+// caller's stream (every call leaves it at zero again). Calls on one device
+// share the array: calls that overlap on one GPU race.
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20; // plans up to this many bytes
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+static void *g_scratch_ptr[64];
+static std::mutex g_scratch_mu;
+
+__global__ __launch_bounds__(256) void zero_words_kernel(int *__restrict__ p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+static int noalloc_scratch(const char *name, hipStream_t st, void **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return set_error(TPP_E_LAUNCH, "%s: no current device", name);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return set_error(TPP_E_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", name,
+                       hipGetErrorString(e));
+    }
+    constexpr int words = (int)(kDecCounterBytes / 4);
+    zero_words_kernel<<<dim3((words + 255) / 256), dim3(256), 0, st>>>((int *)ptr, words);
+    if (int rc = check_launch(name)) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return TPP_OK;
+}
+
+extern "C" int tpp_attn_decode_noalloc(const void *q, const void *k_cache, const void *v_cache,
+                                       void *o, const int64_t *q_strides,
+                                       const int64_t *k_strides, const int64_t *v_strides,
+                                       const int64_t *o_strides, const int32_t *seqlens,
+                                       int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                       int64_t Lmax, float softmax_scale, int window_left,
+                                       int dtype, void *stream) {
+  const char *name = "tpp_attn_decode_noalloc";
+  if (!q_strides || !k_strides || !v_strides || !o_strides)
+    return set_error(TPP_E_INVALID, "%s: null stride array", name);
+  if (B > 0xffff || Hkv > 0xffff || Lmax > 0x7fffffff)
+    return set_error(TPP_E_UNSUPPORTED, "%s: dimension too large", name);
+  AttnArgs a = make_args(q, k_cache, v_cache, o, q_strides, k_strides, v_strides, o_strides, B,
+                         1, Lmax, Hq, Hkv, D, softmax_scale, window_left < 0 ? -1 : window_left,
+                         0);
+  if (int e = check_attn(name, a, D)) return e;
+  if (a.B == 0) return TPP_OK;
+  const size_t need = plan_decode(B, Hq, Hkv, D, Lmax).ws_bytes;
+  if (need > kNoAllocScratchBytes)
+    return set_error(TPP_E_UNSUPPORTED,
+                     "%s: this shape needs %zu bytes of scratch, more than the %zu-byte static "
+                     "array (use tpp_attn_decode with a workspace)",
+                     name, need, kNoAllocScratchBytes);
+  void *ws = nullptr;
+  if (int e = noalloc_scratch(name, as_stream(stream), &ws)) return e;
+  DecodeFuse fz{};
+  // no placement probe here (it reads back to the host): the in-kernel merge
+  // is used once another decode call has verified the placement on this
+  // device, the merge kernel until then
+  return decode_impl(name, a, D, Lmax, seqlens, fz, dtype, ws, kNoAllocScratchBytes, stream,
+                     false);
 }
 
 extern "C" int tpp_attn_decode_fused(const void *qkv, const void *q_norm_w, const void *k_norm_w,
