@@ -137,10 +137,12 @@ def measure_kernels(model, dec, cfg, L):
     t = event_time_us(lambda: C.gemv_argmax(x1, wout, fw, 1e-6, False), 8)
     out.append(hbm_entry("gemv_argmax lm_head +rmsnorm [8x1024]x[151936x1024]^T (+partials)", t,
                          (V * E + B * E) * 2))
-    # per-token QK-norm + RoPE + KV append (bytes fit in the MALL: warm figure)
-    qkv = torch.randn(B, 1, (H + 2 * Hkv) * D, generator=g, device=dev).to(dt)
-    qo = torch.empty(B, 1, H, D, dtype=dt, device=dev)
-    pos = torch.full((B,), L, dtype=torch.int32, device=dev)
+    # prefill shapes. QK-norm + RoPE + KV append of the prefill (the decode
+    # graph does this inside the attention kernel's prologue instead)
+    M = BATCH * PREFILL
+    qkv = torch.randn(B, PREFILL, (H + 2 * Hkv) * D, generator=g, device=dev).to(dt)
+    qo = torch.empty(B, PREFILL, H, D, dtype=dt, device=dev)
+    pos = torch.zeros(B, dtype=torch.int32, device=dev)
     a0 = blocks[0].attn
 
     def rope():
@@ -148,10 +150,10 @@ def measure_kernels(model, dec, cfg, L):
         C.qkv_rope_cache(qkv, qo, c.k_cache, c.v_cache, a0.q_norm.weight, a0.k_norm.weight,
                          model.cos, model.sin, pos, 1e-6)
 
-    t = event_time_us(rope, 2 * nl)
-    out.append(hbm_entry("qkv_rope_cache [8 tokens, 16+8+8 heads]", t, 2 * B * (H + 2 * Hkv) * D * 2 + 4 * B * 2 * D * 2))
-    # prefill shapes (MFMA-bound)
-    M = BATCH * PREFILL
+    t = event_time_us(rope, nl)
+    out.append(hbm_entry("qkv_rope_cache (prefill) [8x2048 tokens, 16+8+8 heads]", t,
+                         2 * M * (H + 2 * Hkv) * D * 2 + 2 * PREFILL * D * 2))
+    del qkv, qo
     xp = torch.randn(M, E, generator=g, device=dev).to(dt)
     t = event_time_us(lambda: C.linear(xp, blocks[cyc()].attn.fused_qkv_weight(), None, 0), nl)
     out.append(mfma_entry("gemm qkv [16384x1024]x[4096x1024]^T", t, 2 * M * 4096 * E))
@@ -198,6 +200,19 @@ def _cfg_entry(cfg_idx, name, bound, cold, warm, amount):
     return e
 
 
+def _copy_ceiling(e, nbytes, sets, randn):
+    """A plain device copy (torch's copy_, one launch) moving the same bytes as
+    an HBM-bound entry (half read, half written), timed the same way: what
+    one launch of this size reaches (launch floor + HBM round trip)."""
+    n = nbytes // 4  # bf16 elements each way
+    nxt = _rotating(lambda i: (randn(n, dtype=torch.bfloat16),
+                               torch.empty(n, dtype=torch.bfloat16, device="cuda")), sets)
+    cold, warm = _cold_warm(lambda a, b: b.copy_(a), nxt, sets)
+    e["copy_us"], e["copy_us_warm"] = round(cold, 3), round(warm, 3)
+    e["kernel_vs_copy"] = round(cold / e["us"], 4)
+    return e
+
+
 def measure_configs():
     """BASELINE.json configs[0..3] at their stated shapes, dtypes and
     distributions (seeded). HBM-bound ops rotate through >= 512 MB of
@@ -218,7 +233,8 @@ def measure_configs():
     w = randn(N, dtype=torch.float16, std=0.1, mean=1.0)
     nxt = _rotating(lambda i: (randn(M, N, dtype=torch.float16),), 40)
     cold, warm = _cold_warm(lambda x: C.rmsnormFused(x, w, 1e-6), nxt, 40)
-    out.append(_cfg_entry(0, "rmsnormFused fp16 [4096x1024]", "hbm", cold, warm, 2 * M * N * 2 + N * 2))
+    out.append(_copy_ceiling(_cfg_entry(0, "rmsnormFused fp16 [4096x1024]", "hbm", cold, warm,
+                                        2 * M * N * 2 + N * 2), 2 * M * N * 2, 40, randn))
     # LayerNorm has no config of its own; same shape
     cold, warm = _cold_warm(lambda x: C.applyLayernorm(x, w, 1e-6), nxt, 40)
     out.append(_cfg_entry(0, "applyLayernorm fp16 [4096x1024]", "hbm", cold, warm, 2 * M * N * 2 + N * 2))
@@ -231,8 +247,8 @@ def measure_configs():
                                randn(1, 8, S, D, dtype=torch.bfloat16)), 24)
     rope_bytes = 2 * (16 + 8) * S * D * 2 + 2 * S * D * 2
     cold, warm = _cold_warm(lambda q, k: C.qkrope_apply_cuda(q, k, cos, sin), nxt, 24)
-    out.append(_cfg_entry(1, "qkrope_apply Q[1,16,2048,128] K[1,8,2048,128] bf16", "hbm", cold, warm,
-                          rope_bytes))
+    out.append(_copy_ceiling(_cfg_entry(1, "qkrope_apply Q[1,16,2048,128] K[1,8,2048,128] bf16", "hbm",
+                                        cold, warm, rope_bytes), 2 * (16 + 8) * S * D * 2, 24, randn))
 
     def inplace(q, k):
         C.rope_apply_(q, cos, sin)
@@ -370,52 +386,106 @@ def cpu_baseline(model, cfg, steps: int = 3):
                       f"(random K/V), after 1 warm-up step; oracle/qwen3.py on the host CPU"}
 
 
-def traffic_probe(L: int, launches: int = 16):
-    """Counter run (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): the
-    roofline kernel at the decode-bench shape (B 8, 16/8 heads, d 128, cache
-    length L) over 8 distinct cache sets (> 512 MB, so reads come from HBM),
-    and a plain 512 MiB device copy whose counter reading calibrates KiB per
-    dispatch against known bytes."""
+TRAFFIC_GROUPS = ["attn", "gemv_qkv", "gemv_o", "gemv_gu", "gemv_down", "lm_head", "rmsnorm",
+                  "layernorm", "rope", "hgemv_3072", "hgemv_1024", "copy"]
+
+
+def traffic_probe(group: str, L: int, launches: int = 16):
+    """Counter run (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE) of one
+    HBM-bound kernel, `launches` times over distinct buffer sets (so no launch
+    finds its bytes in another launch's L2 lines), followed by three plain
+    512 MiB device copies whose counter readings calibrate KiB per dispatch
+    against known bytes. Groups: the decode attention at the decode-bench
+    shape (B 8, 16/8 heads, d 128, cache length L), the four decode GEMVs and
+    the lm_head at the model shapes, and BASELINE configs 0/1/3 (RMSNorm,
+    LayerNorm, Q+K RoPE, both hgemv shapes); `copy` is the calibration alone.
+    Prints the algorithmic bytes per launch."""
     from torchplusplus_amd._native import ext
 
     C = ext()
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(3)
-    B, H, Hkv, D = BATCH, 16, 8, 128
-    sets = [(torch.randn(B, Hkv, L, D, generator=g, device=dev).bfloat16(),
-             torch.randn(B, Hkv, L, D, generator=g, device=dev).bfloat16()) for _ in range(8)]
-    q = torch.randn(B, 1, H, D, generator=g, device=dev).bfloat16()
-    seq = torch.full((B,), L, dtype=torch.int32, device=dev)
-    o = torch.empty_like(q)
+    B, H, Hkv, D, E, I, V = BATCH, 16, 8, 128, 1024, 3072, 151936
+
+    def rn(*shape, dtype=torch.bfloat16, std=1.0):
+        return (std * torch.randn(*shape, generator=g, device=dev)).to(dtype)
+
+    def rot(n, make):
+        sets = [make() for _ in range(n)]
+        return lambda i: sets[i % n]
+
+    launch, nbytes = None, 0
+    if group == "attn":
+        get = rot(8, lambda: (rn(B, Hkv, L, D), rn(B, Hkv, L, D)))
+        q, seq = rn(B, 1, H, D), torch.full((B,), L, dtype=torch.int32, device=dev)
+        o = torch.empty_like(q)
+        launch = lambda i: C.attn_decode(q, *get(i), seq, 0.0, -1, o)  # noqa: E731
+        nbytes = 2 * B * Hkv * L * D * 2 + 2 * B * H * D * 2
+    elif group.startswith("gemv_"):
+        nw = torch.ones(E, dtype=torch.bfloat16, device=dev)
+        res = rn(B, 1, E)
+        n, k, x, call = {
+            "gemv_qkv": (4096, E, rn(B, 1, E), lambda x, w: C.gemv_fused(x, w, nw, 1e-6)),
+            "gemv_o": (E, H * D, rn(B, 1, H * D), lambda x, w: C.gemv_fused(x, w, None, 1e-6, res)),
+            "gemv_gu": (2 * I, E, rn(B, 1, E), lambda x, w: C.gemv_swiglu(x, w, nw, 1e-6)),
+            "gemv_down": (E, I, rn(B, 1, I), lambda x, w: C.gemv_fused(x, w, None, 1e-6, res)),
+        }[group]
+        get = rot(16, lambda: rn(n, k, std=0.02))
+        launch = lambda i: call(x, get(i))  # noqa: E731
+        nbytes = (n * k + B * k + B * n) * 2
+    elif group == "lm_head":
+        get = rot(2, lambda: rn(V, E, std=0.02))
+        x, nw = rn(B, 1, E), torch.ones(E, dtype=torch.bfloat16, device=dev)
+        launch = lambda i: C.gemv_argmax(x, get(i), nw, 1e-6, False)  # noqa: E731
+        nbytes = (V * E + B * E) * 2
+    elif group in ("rmsnorm", "layernorm"):
+        w = rn(E, dtype=torch.float16, std=0.1) + 1
+        get = rot(16, lambda: rn(4096, E, dtype=torch.float16))
+        fn = C.rmsnormFused if group == "rmsnorm" else C.applyLayernorm
+        launch = lambda i: fn(get(i), w, 1e-6)  # noqa: E731
+        nbytes = 2 * 4096 * E * 2 + E * 2
+    elif group == "rope":
+        from torchplusplus_amd.dlops.rope import compute_rope_params
+        cos, sin = compute_rope_params(D, 1e6, 2048, device=dev, out_dtype=torch.bfloat16)
+        get = rot(12, lambda: (rn(1, 16, 2048, D), rn(1, 8, 2048, D)))
+        launch = lambda i: C.qkrope_apply_cuda(*get(i), cos, sin)  # noqa: E731
+        nbytes = 2 * 24 * 2048 * D * 2 + 2 * 2048 * D * 2
+    elif group.startswith("hgemv_"):
+        n = int(group.split("_")[1])
+        k = 4096 - n
+        get = rot(48, lambda: (rn(1, k, dtype=torch.float16), rn(n, k, dtype=torch.float16, std=0.02)))
+        launch = lambda i: C.gemv(*get(i), None, 0)  # noqa: E731
+        nbytes = (n * k + k + n) * 2
+    elif group != "copy":
+        raise SystemExit(f"unknown traffic group {group}")
     src = torch.randn(256 << 20, generator=g, device=dev).bfloat16()  # 512 MiB
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    for i in range(launches):
-        kc, vc = sets[i % 8]
-        C.attn_decode(q, kc, vc, seq, 0.0, -1, o)
+    keep = []
+    if launch is not None:
+        for i in range(launches):
+            keep.append(launch(i))
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"probe": "attn_decode", "B": B, "L": L, "launches": launches,
-                      "algorithmic_bytes": 2 * B * Hkv * L * D * 2 + 2 * B * H * D * 2,
-                      "copy_bytes_each_way": src.numel() * 2}), flush=True)
+    print(json.dumps({"probe": group, "B": B, "L": L, "launches": launches if launch else 0,
+                      "algorithmic_bytes": nbytes, "copy_bytes_each_way": src.numel() * 2}),
+          flush=True)
 
 
 def measured_traffic(cache_len: int):
-    """HBM bytes per launch of the roofline kernel from the committed counter
-    summary (two rocprofv3 --pmc passes calibrated on a copy of known size),
-    when it was measured at this cache length; else None."""
+    """HBM bytes per launch of the roofline kernel from a committed counter
+    summary (two rocprofv3 --pmc passes calibrated on a copy of known size)
+    measured at this cache length; else None."""
+    import glob
     import re
-    path = os.path.join(ROOT, "profiles", "attn_decode_b8_l2176_traffic.md")
-    try:
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "attn_decode_b8_l*_traffic.md"))):
         txt = open(path).read()
-    except OSError:
-        return None
-    b = re.search(r"^traffic_bytes_per_launch: (\d+)$", txt, re.M)
-    L = re.search(r"^traffic_cache_len: (\d+)$", txt, re.M)
-    if not b or not L or int(L.group(1)) != cache_len:
-        return None
-    return int(b.group(1))
+        b = re.search(r"^traffic_bytes_per_launch: (\d+)$", txt, re.M)
+        L = re.search(r"^traffic_cache_len: (\d+)$", txt, re.M)
+        if b and L and int(L.group(1)) == cache_len:
+            return int(b.group(1))
+    return None
 
 
 def kernel_probe(name: str, reps: int = 5):
@@ -438,12 +508,13 @@ def kernel_probe(name: str, reps: int = 5):
             C.LinearSilu(x, w, b)
         for _ in range(reps):
             C.linear(xp, wp, None, 0)
-    elif name == "attn_prefill":
+    elif name in ("attn_prefill", "attn_prefill_window"):
         q = torch.randn(4, 2048, 16, 128, generator=g, device=dev).bfloat16()
         k = torch.randn(4, 2048, 8, 128, generator=g, device=dev).bfloat16()
         v = torch.randn(4, 2048, 8, 128, generator=g, device=dev).bfloat16()
+        left = 511 if name == "attn_prefill_window" else -1
         for _ in range(reps):
-            C.flash_attn_func(q, k, v, True, -1, -1, 0.0)
+            C.flash_attn_func(q, k, v, True, left, -1, 0.0)
     else:
         raise SystemExit(f"unknown probe {name}")
     torch.cuda.synchronize()
@@ -457,9 +528,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=8)
-    ap.add_argument("--traffic-probe", action="store_true",
-                    help="only run the roofline kernel + a calibration copy (for rocprofv3 --pmc)")
-    ap.add_argument("--kernel-probe", choices=["gemm", "attn_prefill"],
+    ap.add_argument("--traffic-probe", nargs="?", const="attn", choices=TRAFFIC_GROUPS,
+                    help="only launch one HBM-bound kernel group + a calibration copy (for "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE); attn at cache length "
+                         "2048 + steps // 2")
+    ap.add_argument("--kernel-probe", choices=["gemm", "attn_prefill", "attn_prefill_window"],
                     help="only launch one config's kernels a few times (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -476,7 +549,7 @@ def main():
     if args.traffic_probe:
         torch.cuda.set_device(0)
         with torch.inference_mode():
-            traffic_probe(PREFILL + args.steps // 2)
+            traffic_probe(args.traffic_probe, PREFILL + args.steps // 2)
         return
 
     from torchplusplus_amd.fastqwen3 import FastQwen3, GreedyDecoder, QwenConfig
