@@ -168,6 +168,35 @@ int tpp_gemv_fused(const void *x, const void *norm_w, float eps, const void *W,
                    void *y, void *residual, int64_t B, int64_t N, int64_t K,
                    int swiglu, int dtype, void *stream);
 
+/* Workspace bytes of tpp_ffn_decode. The workspace must be 256-byte aligned
+ * and zero-filled before its first use: its first 8 KiB hold counters that
+ * every call leaves at zero again (calls of any shape may share it, nothing
+ * else may write those bytes; calls that share it must be ordered). */
+size_t tpp_ffn_decode_workspace_size(int64_t B, int64_t E, int64_t I);
+
+/* The decoder block's FFN half for B <= 16 new tokens, in place on the
+ * residual stream [B, E] (contiguous):
+ *   residual <- T(residual + T(down(T(silu(T(g))) * T(u))))
+ *   g, u = RMSNorm(residual) * norm_w . Wg^T, . Wu^T
+ * replacing rms_norm2 -> ffn -> `x + x_res` of the reference block
+ * (examples/LLM/fastqwen3.py:113-116) with the SwiGLU FFN it intends
+ * (fastqwen3.py:66-79; examples/TTS/dia/model.py:114-116). w_gu is the
+ * interleaved [2I, E] gate/up weight of tpp_linear_swiglu, w_down the
+ * nn.Linear weight [E, I]. For E = 1024, I in {1024, 2048, 3072, 4096} on a
+ * 256-CU device the whole block is one launch (the down projection split
+ * over the 8 XCDs, partials summed in a fixed order); otherwise, or if the
+ * workgroup placement check fails, it is the two GEMV launches
+ * (tpp_gemv_fused with swiglu, then with the residual). */
+int tpp_ffn_decode(void *residual, const void *norm_w, float eps,
+                   const void *w_gu, const void *w_down, int64_t B, int64_t E,
+                   int64_t I, int dtype, void *workspace, size_t ws_bytes,
+                   void *stream);
+
+/* Test hook: *out = nonzero if a tpp_ffn_decode launch on this workspace
+ * ever gave up waiting for its workgroups (never expected; the output of
+ * such a launch is wrong). Synchronises `stream`. */
+int tpp_ffn_decode_sync_errors(const void *workspace, int *out, void *stream);
+
 /* Workspace bytes of tpp_gemv_argmax (no initialisation required). */
 size_t tpp_gemv_argmax_workspace_size(int64_t B, int64_t N);
 

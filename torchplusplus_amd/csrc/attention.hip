@@ -1126,60 +1126,6 @@ static DecodePlan plan_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
   return pl;
 }
 
-// ---- placement check for the in-kernel split merge -------------------------
-// The in-kernel merge relies on workgroups with equal blockIdx % 8 running on
-// one XCD (so their partials and the arrival counter meet in one L2). Once
-// per device a probe launch records HW_REG_XCC_ID for 512 workgroups; if any
-// workgroup's XCD differs from that of workgroup (id % 8), decode falls back
-// to the merge kernel on that device. The probe needs a synchronous read
-// back, so it is skipped (merge kernel for that call, no verdict cached)
-// while the caller's stream is being captured.
-constexpr int kXcdProbeBlocks = 512;
-static __device__ int g_xcd_probe[kXcdProbeBlocks];
-static std::atomic<int> g_xcd_state[64]; // 0 unknown, 1 holds, 2 does not hold
-static std::mutex g_xcd_mu;
-
-__global__ __launch_bounds__(64) void xcd_probe_kernel(int *__restrict__ out) {
-  unsigned v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-  if (threadIdx.x == 0) out[blockIdx.x] = (int)(v & 0xfu);
-}
-
-static bool xcd_grouping_holds(hipStream_t st, bool may_probe) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    (void)hipGetLastError();
-    return false;
-  }
-  int s = g_xcd_state[dev].load(std::memory_order_acquire);
-  if (s || !may_probe) return s == 1;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-    (void)hipGetLastError();
-    return false;
-  }
-  std::lock_guard<std::mutex> lock(g_xcd_mu);
-  s = g_xcd_state[dev].load(std::memory_order_acquire);
-  if (s) return s == 1;
-  int *d = nullptr;
-  int h[kXcdProbeBlocks];
-  hipError_t e = hipGetSymbolAddress((void **)&d, HIP_SYMBOL(g_xcd_probe));
-  if (e == hipSuccess) {
-    xcd_probe_kernel<<<dim3(kXcdProbeBlocks), dim3(64), 0, st>>>(d);
-    e = hipGetLastError();
-  }
-  if (e == hipSuccess) e = hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, st);
-  if (e == hipSuccess) e = hipStreamSynchronize(st);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return false;
-  }
-  bool ok = true;
-  for (int i = 0; i < kXcdProbeBlocks; ++i) ok = ok && h[i] == h[i % 8];
-  g_xcd_state[dev].store(ok ? 1 : 2, std::memory_order_release);
-  return ok;
-}
-
 template <typename T, int D, int G>
 static void launch_decode_g(const AttnArgs &a, dim3 grid, const int *seqlens, int L, float *ws_o,
                             float *ws_ml, int *counters, const DecodePlan &pl, const DecodeFuse &fz,

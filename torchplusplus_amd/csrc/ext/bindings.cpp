@@ -453,10 +453,11 @@ struct ScratchSlot {
 };
 
 at::Tensor cached_workspace(const at::Tensor &like, size_t bytes, int slot = 0) {
-  static std::vector<ScratchSlot> *cache = new std::vector<ScratchSlot>(128);
+  constexpr int kSlots = 3; // 0: greedy-step argmax partials, 1: decode attention, 2: decode FFN
+  static std::vector<ScratchSlot> *cache = new std::vector<ScratchSlot>(64 * kSlots);
   const int dev = like.device().index();
-  TORCH_CHECK(dev >= 0 && dev < 64 && slot >= 0 && slot < 2, "device index out of range");
-  ScratchSlot &e = (*cache)[dev * 2 + slot];
+  TORCH_CHECK(dev >= 0 && dev < 64 && slot >= 0 && slot < kSlots, "device index out of range");
+  ScratchSlot &e = (*cache)[dev * kSlots + slot];
   hipStream_t s = (hipStream_t)cur_stream(like);
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   TORCH_CHECK(hipStreamIsCapturing(s, &cs) == hipSuccess, "hipStreamIsCapturing failed");
@@ -474,6 +475,43 @@ at::Tensor cached_workspace(const at::Tensor &like, size_t bytes, int slot = 0) 
   }
   e.last = capturing ? nullptr : s;
   return e.t;
+}
+
+// decode FFN half of a decoder block, in place on the residual stream
+void ffn_decode(at::Tensor residual, at::Tensor norm_w, double eps, at::Tensor w_gu,
+                at::Tensor w_down) {
+  TORCH_CHECK(residual.is_cuda() && is_half_or_bf16(residual) && residual.is_contiguous(),
+              "residual must be a contiguous CUDA half/bfloat16 tensor [..., E]");
+  const int64_t E = residual.size(-1), B = residual.numel() / E;
+  TORCH_CHECK(B >= 1 && B <= 16, "ffn_decode handles 1 to 16 tokens");
+  TORCH_CHECK(w_gu.dim() == 2 && w_gu.size(1) == E && w_gu.size(0) % 64 == 0 &&
+                  w_gu.is_contiguous() && w_gu.scalar_type() == residual.scalar_type(),
+              "w_gu must be a contiguous [2I, E] interleaved gate/up weight (2I % 64 == 0)");
+  const int64_t I = w_gu.size(0) / 2;
+  TORCH_CHECK(w_down.dim() == 2 && w_down.size(0) == E && w_down.size(1) == I &&
+                  w_down.is_contiguous() && w_down.scalar_type() == residual.scalar_type(),
+              "w_down must be a contiguous [E, I] weight");
+  TORCH_CHECK(norm_w.numel() == E && norm_w.is_contiguous() &&
+                  norm_w.scalar_type() == residual.scalar_type(),
+              "norm weight must be [E] of the residual dtype");
+  c10::DeviceGuard g(residual.device());
+  const size_t wsb = tpp_ffn_decode_workspace_size(B, E, I);
+  at::Tensor ws = cached_workspace(residual, wsb, 2);
+  check_rc(tpp_ffn_decode(residual.data_ptr(), norm_w.data_ptr(), (float)eps, w_gu.data_ptr(),
+                          w_down.data_ptr(), B, E, I, dtype_code(residual), ws.data_ptr(),
+                          (size_t)ws.numel() * 4, cur_stream(residual)),
+           "ffn_decode");
+}
+
+// nonzero if a fused decode FFN launch on this device's workspace ever gave
+// up waiting for its workgroups (test hook; synchronises the stream)
+int64_t ffn_decode_sync_errors(at::Tensor like) {
+  c10::DeviceGuard g(like.device());
+  at::Tensor ws = cached_workspace(like, 1, 2);
+  int out = 0;
+  check_rc(tpp_ffn_decode_sync_errors(ws.data_ptr(), &out, cur_stream(like)),
+           "ffn_decode_sync_errors");
+  return out;
 }
 
 // greedy decode tail: ids <- argmax(lm_head(norm(input))), resid_next <-
@@ -658,6 +696,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("qkv"), py::arg("q_norm_w"), py::arg("k_norm_w"), py::arg("cos"), py::arg("sin"),
         py::arg("eps"), py::arg("k_cache"), py::arg("v_cache"), py::arg("seqlens"),
         py::arg("softmax_scale") = 0.0, py::arg("window_left") = -1);
+  m.def("ffn_decode", &ffn_decode,
+        "decode FFN half of a decoder block (RMSNorm + SwiGLU + down + residual), in place",
+        py::arg("residual"), py::arg("norm_weight"), py::arg("eps"), py::arg("w_gu"),
+        py::arg("w_down"));
+  m.def("ffn_decode_sync_errors", &ffn_decode_sync_errors,
+        "test hook: nonzero if a fused decode FFN launch gave up waiting for its workgroups",
+        py::arg("like"));
   m.def("argmax_rows", &argmax_rows, "argmax over the last dim (greedy sampling)", py::arg("x"));
   m.def("flash_attn_func", &attn_fwd, "flash attention forward (GQA, causal, window)",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("causal") = false,

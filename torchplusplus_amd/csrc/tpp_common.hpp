@@ -184,6 +184,12 @@ template <int ACT> __device__ __forceinline__ float apply_act(float x) {
 // ---- host-side error state -------------------------------------------------
 int set_error(int code, const char *fmt, ...);
 int check_launch(const char *what);
+// Workgroups with equal blockIdx % 8 share an XCD (and its L2) on the current
+// device: measured once per device by a probe launch (tpp_capi.hip); false
+// while unknown when the probe cannot run (stream capture, !may_probe).
+bool xcd_grouping_holds(hipStream_t st, bool may_probe);
+// Compute units of the current device (0 if unknown).
+int device_cu_count();
 __host__ __device__ inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 inline int elem_size(int dtype) { return dtype == TPP_F32 ? 4 : 2; }

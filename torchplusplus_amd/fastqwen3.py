@@ -11,10 +11,11 @@ Execution:
   * forward_impl keeps the residual stream in one buffer. For prefill it
     fuses each residual add into the next RMSNorm; for <= 16 tokens
     (decode) each RMSNorm is fused into the GEMV that reads it, each
-    residual add into the GEMV that writes it, and the QK-norm + RoPE +
-    KV-append of the new token into the decode attention kernel, so a layer
-    is 6 kernels: QKV GEMV, split-KV attention (+merge), o_proj GEMV, SwiGLU
-    GEMV, down GEMV.
+    residual add into the GEMV that writes it, the QK-norm + RoPE +
+    KV-append of the new token into the decode attention kernel, and the
+    whole FFN half (RMSNorm, SwiGLU gate/up, down, residual add) into one
+    launch, so a layer is 4 kernels: QKV GEMV, split-KV attention, o_proj
+    GEMV, FFN.
   * GreedyDecoder captures one whole decode step (28 layers, lm_head,
     argmax, position advance) into a HIP graph and replays it per token, so
     the token loop issues one launch per token and never synchronises.
@@ -176,8 +177,7 @@ class FastQwen3(LLMInference):
             qkv = _C.gemv_fused(resid, at.fused_qkv_weight(), n1.weight, n1.eps)
             o = at.attend(qkv, self.cos, self.sin, kv, cache_position)
             _C.gemv_fused(o, at.out_projection.weight, None, 1e-6, resid)
-            h = _C.gemv_swiglu(resid, blk.ffn.w_gu(), n2.weight, n2.eps)
-            _C.gemv_fused(h, blk.ffn.linear_layer2.weight, None, 1e-6, resid)
+            _C.ffn_decode(resid, n2.weight, n2.eps, blk.ffn.w_gu(), blk.ffn.linear_layer2.weight)
         return _C.gemv_fused(resid, self.out_head.weight, self.final_rmsnorm.weight,
                              self.final_rmsnorm.eps)
 
@@ -224,8 +224,7 @@ class GreedyDecoder:
             qkv = _C.gemv_fused(resid, at.fused_qkv_weight(), n1.weight, n1.eps)
             o = at.decode_fused(qkv, m.cos, m.sin, kc, vc, self.seqlens)
             _C.gemv_fused(o.view(B, 1, at.d_out), at.out_projection.weight, None, 1e-6, resid)
-            h = _C.gemv_swiglu(resid, blk.ffn.w_gu(), n2.weight, n2.eps)
-            _C.gemv_fused(h, blk.ffn.linear_layer2.weight, None, 1e-6, resid)
+            _C.ffn_decode(resid, n2.weight, n2.eps, blk.ffn.w_gu(), blk.ffn.linear_layer2.weight)
         fn = m.final_rmsnorm
         _C.greedy_step(resid, m.out_head.weight, fn.weight, fn.eps, m.tok_embed.weight,
                        self.ids, resid, self.positions, self.seqlens)
