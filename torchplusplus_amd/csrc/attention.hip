@@ -1099,7 +1099,9 @@ static DecodePlan plan_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
   const int64_t pairs = B * Hkv > 0 ? B * Hkv : 1;
   pl.nw = (Hkv > 0 && Hq / Hkv <= 2) ? kDecBigNW : 4; // more query heads per KV head: more VGPRs
   const int64_t batch = pl.nw * kpw * kDecU; // keys per block-wide load batch
-  // about kDecWaves waves, in whole load batches
+  // about kDecWaves waves, in whole load batches (a block's loop runs whole
+  // batches: a chunk of part batches costs the same time with keys masked,
+  // measured 18.3 -> 20.0 us at the model shape with 32-key granularity)
   int64_t want = (kDecWaves / pl.nw + pairs - 1) / pairs;
   int64_t chunk = (Lmax + want - 1) / want;
   chunk = ((chunk + batch - 1) / batch) * batch;

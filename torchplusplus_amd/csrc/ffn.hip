@@ -199,7 +199,7 @@ __global__ __launch_bounds__(256) void ffn_decode_kernel(FfnArgs a) {
         xa[u][i] = from_f32<T>((to_f32(xa[u][i]) * inv) * to_f32(nwv[u][i]));
     // gate/up weights landed (the down DMA may still be in flight); the
     // operand reads are inline asm so no compiler wait covers that DMA
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (U2 / 2)); // vmcnt(U2 / 2)
+    vm_wait<U2 / 2>();
     const unsigned gbase = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char *)gslot;
     V8 wg[kFfnNS1], wu[kFfnNS1];
 #pragma unroll

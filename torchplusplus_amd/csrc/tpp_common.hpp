@@ -195,6 +195,13 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 inline int elem_size(int dtype) { return dtype == TPP_F32 ? 4 : 2; }
 inline bool half_type(int dtype) { return dtype == TPP_F16 || dtype == TPP_BF16; }
 
+// s_waitcnt vmcnt(N) alone (N < 64; the count is split over two fields of
+// the instruction's immediate, bits 3:0 and 15:14)
+template <int N> __device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
 // Workgroup barrier for data exchanged through LDS by ds_write/ds_read: waits
 // for this wave's LDS accesses (lgkmcnt(0)) but, unlike the fenced
 // __syncthreads(), not for LDS-DMA (global_load_lds) still in flight.
@@ -217,6 +224,12 @@ template <int OFF> __device__ __forceinline__ s16x4 lds_read_tr16(unsigned addr)
   static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
   s16x4 r;
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+template <int OFF> __device__ __forceinline__ float lds_read_b32(unsigned addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  float r;
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
   return r;
 }
 template <int OFF, typename V> __device__ __forceinline__ V lds_read_b128(unsigned addr) {
