@@ -55,6 +55,9 @@ constexpr int kSmallBK = TPP_SMALL_BK, kSmallNST = TPP_SMALL_NST;
 // below this many outputs the register-staged kernel's smaller LDS footprint
 // (several blocks per CU) wins over the deeper DMA ring
 constexpr int64_t kDmaMinMN = 256 * 128 * 128;
+// the DMA kernel addresses a tile's rows by 32-bit byte offsets from its
+// first row: 256 rows * ld * 2 bytes stays below 2^32 up to this pitch
+constexpr int64_t kDmaMaxLd = 1 << 22;
 
 template <typename T>
 __device__ __forceinline__ f32x16 mfma32(typename VecT<T>::v8 a, typename VecT<T>::v8 b,
@@ -251,31 +254,32 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
   // w and i only (NWV is even). Source rows are clamped to the matrix: rows
   // past M / N only feed outputs that are never stored.
   const int lrow = lane / CPR, lkc = (lane % CPR) ^ swzk<BK>(RPI * w + lrow);
-  const int arow = m0 + w * RPI + lrow, brow = n0 + w * RPI + lrow;
-  auto issue = [&](int stage, int kt) {
-    V8 *sa = smem + stage * STG, *sb = sa + BM * CPR;
-    const int64_t ko = (int64_t)kt * BK + lkc * 8;
+  // DMA sources: a uniform tile base (row m0 of A, row n0 of B, in scalar
+  // registers) plus per-lane 32-bit byte offsets of the lane's clamped rows
+  // relative to it, fixed for the whole K loop (the host keeps
+  // BM * ld * sizeof(T) below 2^32)
+  constexpr int NQ = NA + NB;
+  const char *ta = reinterpret_cast<const char *>(A) + (int64_t)m0 * lda * (int64_t)sizeof(T);
+  const char *tb = reinterpret_cast<const char *>(B) + (int64_t)n0 * ldb * (int64_t)sizeof(T);
+  uint32_t off[NQ];
 #pragma unroll
-    for (int j = 0; j < NA; ++j)
-      __builtin_amdgcn_global_load_lds((const void *)(A + (int64_t)min(arow + RPI * NWV * j, M - 1) * lda + ko),
-                                       (__attribute__((address_space(3))) void *)(sa + (j * NWV + w) * 64),
-                                       16, 0, 0);
+  for (int q = 0; q < NA; ++q)
+    off[q] = (uint32_t)((int64_t)(min(m0 + w * RPI + lrow + RPI * NWV * q, M - 1) - m0) * lda + lkc * 8) *
+             (uint32_t)sizeof(T);
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
-      __builtin_amdgcn_global_load_lds((const void *)(B + (int64_t)min(brow + RPI * NWV * j, N - 1) * ldb + ko),
-                                       (__attribute__((address_space(3))) void *)(sb + (j * NWV + w) * 64),
-                                       16, 0, 0);
-  };
-  // DMA instruction q (0 .. NA + NB - 1) of tile kt into a stage
+  for (int q = 0; q < NB; ++q)
+    off[NA + q] = (uint32_t)((int64_t)(min(n0 + w * RPI + lrow + RPI * NWV * q, N - 1) - n0) * ldb + lkc * 8) *
+                  (uint32_t)sizeof(T);
+  // DMA instruction q (0 .. NQ - 1) of K tile kt into a stage
   auto issue_one = [&](int stage, int kt, int q) {
     V8 *sa = smem + stage * STG, *sb = sa + BM * CPR;
-    const int64_t ko = (int64_t)kt * BK + lkc * 8;
+    const int64_t kb = (int64_t)kt * BK * sizeof(T);
     if (q < NA)
-      __builtin_amdgcn_global_load_lds((const void *)(A + (int64_t)min(arow + RPI * NWV * q, M - 1) * lda + ko),
+      __builtin_amdgcn_global_load_lds((const void *)(ta + kb + off[q]),
                                        (__attribute__((address_space(3))) void *)(sa + (q * NWV + w) * 64),
                                        16, 0, 0);
     else
-      __builtin_amdgcn_global_load_lds((const void *)(B + (int64_t)min(brow + RPI * NWV * (q - NA), N - 1) * ldb + ko),
+      __builtin_amdgcn_global_load_lds((const void *)(tb + kb + off[q]),
                                        (__attribute__((address_space(3))) void *)(sb + ((q - NA) * NWV + w) * 64),
                                        16, 0, 0);
   };
@@ -309,56 +313,57 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
       }
   }
 
+  // Main loop. Each K tile is KS = BK/16 sub-steps of FM x FN MFMAs, with
+  // the operand fragments of sub-step ks + 1 read (into the other register
+  // set) while the MFMAs of ks run. The DMA of K tile kt + NST - 1 goes into
+  // the slot every wave finished reading before the last barrier and is
+  // spread between the MFMAs of the first half of the tile, so no wave
+  // stalls on a burst of DMA issue. The wait for K tile kt + 1's DMA and the
+  // barrier that publishes it sit in the middle of the last sub-step, right
+  // before the next tile's first fragment reads: the second half of the
+  // sub-step's MFMAs is still to issue while the barrier resolves and those
+  // reads return (measured 3-4% faster on the prefill shapes than a barrier
+  // at the top of each K tile).
+  constexpr int KS = BK / 16;
+  static_assert(KS % 2 == 0, "register sets alternate across the K-tile boundary");
+  constexpr int NMF = KS * FM * FN;
+  constexpr int MID = NMF - (FM * FN) / 2; // MFMAs of a K tile issued before its barrier
+  constexpr int SP = (NMF / 2) / NQ > 0 ? (NMF / 2) / NQ : 1; // MFMAs per DMA instruction
+  static_assert(NQ * SP <= MID, "all DMA of a K tile issued before its barrier");
   const int nk = K / BK;
 #pragma unroll
   for (int p = 0; p < NST - 1; ++p)
-    if (p < nk) issue(p, p);
-  for (int kt = 0; kt < nk; ++kt) {
-    // own DMA of tile kt complete (later tiles may still be in flight), own
-    // reads of tile kt-1 complete; then the barrier publishes both
-    if constexpr (NST == 2) {
-      wait_vmcnt<0>();
-    } else {
-      // tiles kt+1 .. kt+NST-2 may still be in flight (fewer near the end)
-      const int ahead = nk - 1 - kt < NST - 2 ? nk - 1 - kt : NST - 2;
-      if (ahead >= NST - 2)
-        wait_vmcnt<(NST - 2) * (NA + NB)>();
-      else if (NST > 3 && ahead == 1)
-        wait_vmcnt<(NA + NB)>();
-      else
-        wait_vmcnt<0>();
+    if (p < nk)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) issue_one(p, p, q);
+  // K tile 0 landed (tile 1 may be in flight)
+  if constexpr (NST == 2) wait_vmcnt<0>();
+  else if (nk > 1) wait_vmcnt<(NST - 2) * NQ>();
+  else wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  V8 af[2][FM], bfr[2][FN];
+  auto frag = [&](const V8 *sa, int ks) {
+    const V8 *sb = sa + BM * CPR;
+    const int kc = ks * 2 + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int row = wm * FM * 32 + i * 32 + (lane & 31);
+      af[ks & 1][i] = sa[row * CPR + (kc ^ swzk<BK>(row))];
     }
-    wait_lgkmcnt0();
-    __builtin_amdgcn_s_barrier();
-    const V8 *sa = smem + (kt % NST) * STG, *sb = sa + BM * CPR;
-    // operand fragments of K sub-step ks into register set ks & 1: the reads
-    // of sub-step ks + 1 are in flight while the MFMAs of ks run
-    V8 af[2][FM], bfr[2][FN];
-    auto frag = [&](int ks) {
-      const int kc = ks * 2 + (lane >> 5);
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int row = wm * FM * 32 + i * 32 + (lane & 31);
-        af[ks & 1][i] = sa[row * CPR + (kc ^ swzk<BK>(row))];
-      }
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int col = wn * FN * 32 + j * 32 + (lane & 31);
-        bfr[ks & 1][j] = sb[col * CPR + (kc ^ swzk<BK>(col))];
-      }
-    };
-    frag(0);
-    // the next tile's DMA (into a stage every wave finished reading before
-    // the barrier) is spread between the MFMAs of the first three quarters
-    // of the step, so no wave stalls on a burst of DMA issue while the MFMA
-    // pipe waits
+    for (int j = 0; j < FN; ++j) {
+      const int col = wn * FN * 32 + j * 32 + (lane & 31);
+      bfr[ks & 1][j] = sb[col * CPR + (kc ^ swzk<BK>(col))];
+    }
+  };
+  frag(smem, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const V8 *sa = smem + (kt % NST) * STG;
     const int kn = kt + NST - 1;
-    const bool more = kn < nk;
-    constexpr int NQ = NA + NB, NMF = (BK / 16) * FM * FN;
-    constexpr int SP = (NMF * 3 / 4) / NQ > 0 ? (NMF * 3 / 4) / NQ : 1;
+    const bool more = kn < nk, next = kt + 1 < nk;
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      if (ks + 1 < BK / 16) frag(ks + 1);
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) frag(sa, ks + 1);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -366,12 +371,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
           acc[i][j] = mfma32<T>(bfr[ks & 1][j], af[ks & 1][i], acc[i][j]);
           const int m = (ks * FM + i) * FN + j + 1;
           if (m % SP == 0 && m / SP <= NQ && more) issue_one(kn % NST, kn, m / SP - 1);
+          if (m == MID && next) {
+            // own DMA of K tile kt + 1 landed (tile kt + 2's may still be in
+            // flight); the fragment reads of tile kt all returned (the MFMAs
+            // above consumed them), so after the barrier its slot may be
+            // refilled by any wave
+            if constexpr (NST == 2) wait_vmcnt<0>();
+            else if (kt + 2 < nk) wait_vmcnt<(NST - 2) * NQ>();
+            else wait_vmcnt<0>();
+            __builtin_amdgcn_s_barrier();
+            frag(smem + ((kt + 1) % NST) * STG, 0);
+          }
         }
-    }
-    if constexpr (NMF / SP < NQ) {
-#pragma unroll
-      for (int q = NMF / SP; q < NQ; ++q)
-        if (more) issue_one(kn % NST, kn, q);
     }
   }
 
@@ -532,7 +543,7 @@ static int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, v
   if (M == 0) return TPP_OK;
   const bool vec = (K % 8 == 0) && (lda % 8 == 0) && (ldb % 8 == 0) && aligned16(A) &&
                    aligned16(B);
-  if (vec && K % 64 == 0 && M * N >= (int64_t)kDmaMinMN) {
+  if (vec && K % 64 == 0 && M * N >= (int64_t)kDmaMinMN && lda <= kDmaMaxLd && ldb <= kDmaMaxLd) {
     if ((M + 127) / 128 * ((N + 127) / 128) > 0x7fffffffLL)
       return set_error(TPP_E_UNSUPPORTED, "%s: too many tiles", name);
     switch (pick_dma_tile(M, N, EPI == kGSwiGLU, device_cus())) {
