@@ -127,11 +127,17 @@ def measure_kernels(model, dec, cfg, L):
     res = torch.randn(B, 1, E, generator=g, device=dev).to(dt)
     gemv_entry("gemv o_proj +residual [8x2048]x[1024x2048]^T", lambda b: b.attn.out_projection.weight,
                E, H * D, xo, lambda a, b: C.gemv_fused(a, b, None, 1e-6, res))
-    gemv_entry("gemv_swiglu gate/up +rmsnorm [8x1024]x[6144x1024]^T", lambda b: b.ffn.w_gu(), 2 * I, E,
-               x1, lambda a, b: C.gemv_swiglu(a, b, nw, 1e-6))
-    xd = torch.randn(B, 1, I, generator=g, device=dev).to(dt)
-    gemv_entry("gemv down +residual [8x3072]x[1024x3072]^T", lambda b: b.ffn.linear_layer2.weight, E, I,
-               xd, lambda a, b: C.gemv_fused(a, b, None, 1e-6, res))
+    # the decode step's FFN half: RMSNorm + gate/up SwiGLU + down + residual in
+    # one launch (weights of all 28 layers in turn, residual updated in place)
+    resf = torch.randn(B, 1, E, generator=g, device=dev).to(dt)
+
+    def ffn():
+        blk = blocks[cyc()]
+        C.ffn_decode(resf, nw, 1e-6, blk.ffn.w_gu(), blk.ffn.linear_layer2.weight)
+
+    t = event_time_us(ffn, nl)
+    out.append(hbm_entry("ffn_decode (RMSNorm + gate/up SwiGLU + down + residual, one launch) "
+                         "[8x1024], I 3072", t, (3 * I * E + 2 * B * E) * 2))
     wout = model.out_head.weight
     fw = model.final_rmsnorm.weight
     t = event_time_us(lambda: C.gemv_argmax(x1, wout, fw, 1e-6, False), 8)
@@ -386,7 +392,7 @@ def cpu_baseline(model, cfg, steps: int = 3):
                       f"(random K/V), after 1 warm-up step; oracle/qwen3.py on the host CPU"}
 
 
-TRAFFIC_GROUPS = ["attn", "gemv_qkv", "gemv_o", "gemv_gu", "gemv_down", "lm_head", "rmsnorm",
+TRAFFIC_GROUPS = ["attn", "gemv_qkv", "gemv_o", "gemv_gu", "gemv_down", "ffn", "lm_head", "rmsnorm",
                   "layernorm", "rope", "hgemv_3072", "hgemv_1024", "copy"]
 
 
@@ -396,8 +402,8 @@ def traffic_probe(group: str, L: int, launches: int = 16):
     finds its bytes in another launch's L2 lines), followed by three plain
     512 MiB device copies whose counter readings calibrate KiB per dispatch
     against known bytes. Groups: the decode attention at the decode-bench
-    shape (B 8, 16/8 heads, d 128, cache length L), the four decode GEMVs and
-    the lm_head at the model shapes, and BASELINE configs 0/1/3 (RMSNorm,
+    shape (B 8, 16/8 heads, d 128, cache length L), the four decode GEMVs, the
+    fused decode FFN and the lm_head at the model shapes, and BASELINE configs 0/1/3 (RMSNorm,
     LayerNorm, Q+K RoPE, both hgemv shapes); `copy` is the calibration alone.
     Prints the algorithmic bytes per launch."""
     from torchplusplus_amd._native import ext
@@ -433,6 +439,12 @@ def traffic_probe(group: str, L: int, launches: int = 16):
         get = rot(16, lambda: rn(n, k, std=0.02))
         launch = lambda i: call(x, get(i))  # noqa: E731
         nbytes = (n * k + B * k + B * n) * 2
+    elif group == "ffn":
+        nw = torch.ones(E, dtype=torch.bfloat16, device=dev)
+        res = rn(B, 1, E)
+        get = rot(16, lambda: (rn(2 * I, E, std=0.02), rn(E, I, std=0.02)))
+        launch = lambda i: C.ffn_decode(res, nw, 1e-6, *get(i))  # noqa: E731
+        nbytes = (3 * I * E + 2 * B * E) * 2
     elif group == "lm_head":
         get = rot(2, lambda: rn(V, E, std=0.02))
         x, nw = rn(B, 1, E), torch.ones(E, dtype=torch.bfloat16, device=dev)

@@ -643,8 +643,8 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
     for (int u = 0; u < U; ++u) {
       const int key0 = base + u * NW * KPW + row;
       const int key = key0 < last ? key0 : last;
-      kr[u] = *reinterpret_cast<const V8 *>(kp + (int64_t)key * p.k_ss);
-      vr[u] = *reinterpret_cast<const V8 *>(vp + (int64_t)key * p.v_ss);
+      kr[u] = ld_nt(reinterpret_cast<const V8 *>(kp + (int64_t)key * p.k_ss));
+      vr[u] = ld_nt(reinterpret_cast<const V8 *>(vp + (int64_t)key * p.v_ss));
     }
   };
   // The first two batches of the chunk go out before the sequence length is

@@ -162,7 +162,8 @@ __global__ __launch_bounds__(256) void ffn_decode_kernel(FfnArgs a) {
         const T *src = Wgu + (grow + set * 32 + row) * kFfnE + w * kFfnKW1 + (dpos ^ row) * 8;
         __builtin_amdgcn_global_load_lds(
             (const void *)src,
-            (__attribute__((address_space(3))) void *)(gslot + set * 512 + jj * 64), 16, 0, 0);
+            (__attribute__((address_space(3))) void *)(gslot + set * 512 + jj * 64), 16, 0,
+            kCpolNT);
       }
   }
 #pragma unroll
@@ -171,7 +172,8 @@ __global__ __launch_bounds__(256) void ffn_decode_kernel(FfnArgs a) {
     const int row = q / U2, unit = q % U2;
     const T *src = Wd + (int64_t)(kFfnRows2 * j + row) * I + x * IX + w * KW2 + unit * 8;
     __builtin_amdgcn_global_load_lds(
-        (const void *)src, (__attribute__((address_space(3))) void *)(dslot + jj * 64), 16, 0, 0);
+        (const void *)src, (__attribute__((address_space(3))) void *)(dslot + jj * 64), 16, 0,
+        kCpolNT);
   }
   __builtin_amdgcn_sched_barrier(0);
 

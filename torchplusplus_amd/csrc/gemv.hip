@@ -215,7 +215,8 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
         kk = kk < K - 8 ? kk : K - 8;
         __builtin_amdgcn_global_load_lds(
             (const void *)(W + gr * K + kk),
-            (__attribute__((address_space(3))) void *)(wslot + set * (RT * 32) + j * 64), 16, 0, 0);
+            (__attribute__((address_space(3))) void *)(wslot + set * (RT * 32) + j * 64), 16, 0,
+            kCpolNT);
       }
     }
     if constexpr (EPI == kEpiResidual) {
@@ -592,7 +593,7 @@ __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tile
       const int64_t k = (int64_t)c * 256 + (dpos ^ row) * 8;
       __builtin_amdgcn_global_load_lds((const void *)(W + wr * K + k),
                                        (__attribute__((address_space(3))) void *)(dst + j * 64),
-                                       16, 0, 0);
+                                       16, 0, kCpolNT);
     }
   };
   if (nchunks > 0) {

@@ -52,8 +52,8 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
   for (int j = 0; j < MAXV; ++j) {
     const int c = j * LPR + l;
     const int64_t cc = (int64_t)(c < nvec ? c : nvec - 1) * 8;
-    xr[j] = *reinterpret_cast<const V8 *>(x + rowc * ldx + cc);
-    if constexpr (MODE == kAddRms) rr[j] = *reinterpret_cast<const V8 *>(resid + rowc * ldy + cc);
+    xr[j] = ld_nt(reinterpret_cast<const V8 *>(x + rowc * ldx + cc));
+    if constexpr (MODE == kAddRms) rr[j] = ld_nt(reinterpret_cast<const V8 *>(resid + rowc * ldy + cc));
     if constexpr (kOut) wr[j] = *reinterpret_cast<const V8 *>(w + cc);
     if constexpr (MODE == kLayer) br[j] = *reinterpret_cast<const V8 *>((b ? b : w) + cc);
   }

@@ -52,8 +52,8 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(
   const int s = (int)(row % S);
   const int64_t base = row * D;
   float x1[8], x2[8], c1[8], c2[8], s1[8], s2[8];
-  load8(src + base + i0, x1);
-  load8(src + base + h + i0, x2);
+  load8_nt(src + base + i0, x1);
+  load8_nt(src + base + h + i0, x2);
   load_cs8(cos + (int64_t)s * D + i0, c1);
   load_cs8(cos + (int64_t)s * D + h + i0, c2);
   load_cs8(sin + (int64_t)s * D + i0, s1);

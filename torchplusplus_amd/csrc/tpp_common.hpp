@@ -74,6 +74,26 @@ __device__ __forceinline__ void store8(T *p, const float (&v)[8]) {
   *reinterpret_cast<V *>(p) = t;
 }
 
+// ---- streaming loads ---------------------------------------------------------
+// Data a launch reads exactly once (decode weights, the KV cache in decode,
+// norm and RoPE input rows) is loaded non-temporal (the NT bit of the cache
+// policy). Measured on MI355X: 16-byte streaming reads of 64 MiB - 1 GiB run
+// at 5.97-7.0 TB/s with it against 5.4-6.2 TB/s without, and LDS-DMA at 6.5
+// against 6.0 TB/s. Data that several workgroups re-read (GEMM operands,
+// prefill K/V tiles, GEMV input rows, norm weights, RoPE tables) keeps the
+// default policy.
+constexpr int kCpolNT = 2; // cache-policy operand of global_load_lds: NT
+template <typename V> __device__ __forceinline__ V ld_nt(const V *p) {
+  return __builtin_nontemporal_load(p);
+}
+template <typename T>
+__device__ __forceinline__ void load8_nt(const T *p, float (&v)[8]) {
+  typedef typename VecT<T>::v8 V;
+  const V t = ld_nt(reinterpret_cast<const V *>(p));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = to_f32(t[i]);
+}
+
 // ---- wave64 reductions -----------------------------------------------------
 // DPP controls (GFX9 encoding): quad_perm, row_half_mirror, row_mirror.
 constexpr int kDppQuadXor1 = 0xB1; // quad_perm [1,0,3,2]
