@@ -560,13 +560,32 @@ template <int N> __device__ __forceinline__ void gemv_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// s_waitcnt vmcnt(N) tied to every register of a (M a multiple of 8): the
+// wait redefines the first eight, empty statements after it (kept in order:
+// all are volatile) the rest, so no use of any of them moves above the wait
+template <int N, typename V, int M>
+__device__ __forceinline__ void vm_wait_tied_all(V (&a)[M]) {
+  static_assert(N >= 0 && N < 64 && M % 8 == 0, "vmcnt is 6 bits; whole groups of 8");
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]),
+                 "+v"(a[6]), "+v"(a[7])
+               : "n"(N));
+#pragma unroll
+  for (int i = 8; i < M; i += 8)
+    asm volatile(""
+                 : "+v"(a[i]), "+v"(a[i + 1]), "+v"(a[i + 2]), "+v"(a[i + 3]), "+v"(a[i + 4]),
+                   "+v"(a[i + 5]), "+v"(a[i + 6]), "+v"(a[i + 7]));
+}
+
 template <typename T, bool NORM, int KC>
 __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tiles) {
   typedef typename VecT<T>::v8 V8;
+  constexpr int NWD = (KC * 32 + 63) / 64; // norm weight DMA instructions (64 units each)
   __shared__ V8 ring[4][kWideRing][16 * 32]; // [wave][slot][row * 32 + (unit ^ row)]
+  __shared__ V8 s_nw[4][NWD * 64];           // [wave][16-byte unit of the norm weight]
   __shared__ float s_bv[4][16];
   __shared__ int s_bi[4][16];
-  const int lane = lane_id(), w = wave_id();
+  const int lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
   const int r = lane & 15, g = lane >> 4;
   const int64_t K = a.K, N = a.N;
   const T *X = (const T *)a.x;
@@ -576,43 +595,65 @@ __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tile
   const int64_t my_tiles = wg < tiles ? (tiles - 1 - wg) / nwg + 1 : 0;
   const int64_t nchunks = my_tiles * KC;
 
-  // DMA of chunk n into ring slot n % kWideRing. Instruction j covers rows
-  // 2j, 2j+1; lane i lands at slot offset i and so fetches unit
-  // (i % 32) ^ row of row 2j + i / 32. Past the end of the stream the
-  // last chunk is fetched again, so every wave keeps the same issue pattern.
-  const int drow = lane >> 5, dpos = lane & 31;
-  auto issue = [&](int64_t n) {
-    const int64_t nn = n < nchunks ? n : nchunks - 1;
-    const int64_t tile = wg + (nn / KC) * nwg;
-    const int c = (int)(nn % KC);
-    V8 *dst = ring[w][(int)(n % kWideRing)];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = 2 * j + drow;
-      const int64_t wr = tile * 16 + row < N ? tile * 16 + row : N - 1;
-      const int64_t k = (int64_t)c * 256 + (dpos ^ row) * 8;
-      __builtin_amdgcn_global_load_lds((const void *)(W + wr * K + k),
-                                       (__attribute__((address_space(3))) void *)(dst + j * 64),
-                                       16, 0, kCpolNT);
-    }
-  };
-  if (nchunks > 0) {
-#pragma unroll
-    for (int p = 0; p < kWideRing - 1; ++p) issue(p);
-  }
-
-  // input rows (<= 16) as A fragments for all K (K = 256 KC): step u covers
-  // k = 32u + 8g, so lanes r, r+16, r+32, r+48 hold all of row r and the
-  // row statistics need no loads of their own. The input loads go out
-  // together with the ring's first DMA (one memory round trip for both; a
-  // separate statistics pass and a barrier would cost two more), the norm
-  // weight (2 KB, shared by every block) once the statistics are known.
+  // Input rows (<= 16) as A fragments for all K (K = 256 KC): step u covers
+  // k = 32u + 8g, so lanes r, r+16, r+32, r+48 hold all of row r and the row
+  // statistics need no loads of their own. These loads go out first, as
+  // inline asm, then the norm weight and the first weight chunks by LDS-DMA:
+  // loads complete in issue order, so counted waits take the input, then the
+  // norm weight, while the weights stream in behind them (after an LDS-DMA
+  // the compiler's own wait for a plain load would be vmcnt(0)).
   const bool xok = r < a.NB;
   const T *xr = X + (xok ? r : 0) * a.ldx;
   V8 xa[KC * 8];
 #pragma unroll
-  for (int u = 0; u < KC * 8; ++u) xa[u] = ld16(xr + (int64_t)u * 32 + g * 8, xok);
-  __builtin_amdgcn_sched_barrier(0); // all of them out before the first use
+  for (int u = 0; u < KC * 8; ++u) xa[u] = ld16_asm(xr + (int64_t)u * 32 + g * 8, xok);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (NORM) {
+    // K / 8 units of 16 bytes into this wave's LDS (lanes past them fetch the
+    // last unit again into the array's padding)
+#pragma unroll
+    for (int i = 0; i < NWD; ++i) {
+      const int unit = i * 64 + lane < KC * 32 ? i * 64 + lane : KC * 32 - 1;
+      __builtin_amdgcn_global_load_lds((const void *)((const T *)a.norm_w + unit * 8),
+                                       (__attribute__((address_space(3))) void *)&s_nw[w][i * 64],
+                                       16, 0, 0);
+    }
+  }
+
+  // DMA of chunk n (16 rows x 256 k of tile wg + (n / KC) nwg) into ring slot
+  // n % kWideRing. Instruction j covers rows 2j, 2j+1; lane i lands at slot
+  // offset i and so fetches unit (i % 32) ^ row of row 2j + i / 32. Source:
+  // the tile's first row (wave-uniform) plus a per-lane 32-bit byte offset;
+  // rows past N read row N-1 (finite data, never stored). Past the end of the
+  // stream the last chunk is fetched again, so every wave keeps the same
+  // issue pattern.
+  const int drow = lane >> 5, dpos = lane & 31;
+  unsigned xo[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) xo[j] = (unsigned)((dpos ^ (2 * j + drow)) * 8 * (int)sizeof(T));
+  const unsigned rowb = (unsigned)(K * (int64_t)sizeof(T)); // bytes per weight row
+  auto issue = [&](int64_t n) {
+    const int64_t nn = n < nchunks ? n : nchunks - 1;
+    const int64_t tile = nn >= 0 ? wg + (nn / KC) * nwg : 0;
+    const int c = nn >= 0 ? (int)(nn % KC) : 0;
+    const char *tb = reinterpret_cast<const char *>(W + tile * 16 * K) + c * 256 * (int)sizeof(T);
+    const int lim = (int)(N - 1 - tile * 16); // last row of the matrix, relative to the tile
+    V8 *dst = ring[w][(int)(n % kWideRing)];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = 2 * j + drow;
+      const unsigned off = (unsigned)(row < lim ? row : lim) * rowb + xo[j];
+      __builtin_amdgcn_global_load_lds((const void *)(tb + off),
+                                       (__attribute__((address_space(3))) void *)(dst + j * 64),
+                                       16, 0, kCpolNT);
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < kWideRing - 1; ++p) issue(p);
+
+  // the input landed (norm weight and weight chunks may be in flight)
+  constexpr int NDMA0 = (NORM ? NWD : 0) + (kWideRing - 1) * 8;
+  vm_wait_tied_all<NDMA0>(xa);
   if constexpr (NORM) {
     float ss = 0.f;
 #pragma unroll
@@ -625,14 +666,16 @@ __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tile
     ss += __shfl_xor(ss, 16, kWave);
     ss += __shfl_xor(ss, 32, kWave);
     const float inv = rsqrtf(ss / (float)K + a.eps);
-    // 8 steps' norm weights per batch of loads: one (L2) round trip per
-    // batch, at 32 extra registers
+    // the norm weight landed in LDS; read back as asm (the compiler would
+    // wait for every LDS-DMA in flight before a plain LDS read)
+    gemv_wait_vmcnt<(kWideRing - 1) * 8>();
+    const unsigned nwb = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char *)&s_nw[w][0];
 #pragma unroll
     for (int u0 = 0; u0 < KC * 8; u0 += 8) {
       V8 nw8[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) nw8[u] = ld16((const T *)a.norm_w + (int64_t)(u0 + u) * 32 + g * 8, true);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int u = 0; u < 8; ++u) nw8[u] = lds_read_b128<0, V8>(nwb + (unsigned)(((u0 + u) * 4 + g) * 16));
+      lds_wait_tied<0>(nw8);
 #pragma unroll
       for (int u = 0; u < 8; ++u)
 #pragma unroll
@@ -644,6 +687,14 @@ __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tile
   float bv[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   int bi[4] = {0x7fffffff, 0x7fffffff, 0x7fffffff, 0x7fffffff};
   T *Y = (T *)a.y;
+  // MFMA operands from the ring by inline-asm LDS reads with explicit waits:
+  // the compiler's wait-count pass cannot tell which slot an LDS-DMA writes
+  // and, for plain reads, waited for all of them (vmcnt(0)) once per tile,
+  // draining the ring
+  const unsigned rbase = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char *)&ring[w][0][0];
+  unsigned roff[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) roff[u] = (unsigned)((r * 32 + ((u * 4 + g) ^ r)) * 16);
   for (int64_t ti = 0; ti < my_tiles; ++ti) {
     const int64_t tile = wg + ti * nwg;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -651,15 +702,16 @@ __global__ __launch_bounds__(256) void gemv_wide_kernel(GemvArgs a, int64_t tile
     for (int c = 0; c < KC; ++c) {
       const int64_t n = ti * KC + c;
       gemv_wait_vmcnt<(kWideRing - 2) * 8>(); // chunk n landed (own DMA)
-      const V8 *src = ring[w][(int)(n % kWideRing)];
+      // refill the slot read at step n - 1 first (its reads completed: the
+      // MFMAs of that step consumed them)
+      issue(n + kWideRing - 1);
+      const unsigned sb = rbase + (unsigned)(n % kWideRing) * (16 * 32 * 16);
       V8 b[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) b[u] = src[r * 32 + ((u * 4 + g) ^ r)];
+      for (int u = 0; u < 8; ++u) b[u] = lds_read_b128<0, V8>(sb + roff[u]);
+      lds_wait_tied<0>(b);
 #pragma unroll
       for (int u = 0; u < 8; ++u) acc = mfma16<T>(xa[c * 8 + u], b[u], acc);
-      // the slot read last is refilled only after those reads completed
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      issue(n + kWideRing - 1);
     }
     // D layout of 16x16x32: lane -> weight row tile*16 + r, rows b = 4g + i
     const int64_t col = tile * 16 + r;
