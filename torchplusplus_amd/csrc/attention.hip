@@ -190,24 +190,28 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
   constexpr int KDMA = kKvTile / KPI / NWL;     // DMA instructions per wave per tile
   const int wu = __builtin_amdgcn_readfirstlane(w) % NWL; // wave index within its group
   const int dkey = lane / CPR, dslot = lane % CPR;
-  unsigned koff[KDMA], voff[KDMA];
+  // Offsets of full tiles, and of the last tile when Sk is not a multiple of
+  // the tile: its keys past Sk read key Sk-1 (the clamp computed here once,
+  // not per tile)
+  const int kb_last = ((p.Sk - 1) / kKvTile) * kKvTile;
+  unsigned koff[KDMA], voff[KDMA], koffl[KDMA], voffl[KDMA];
 #pragma unroll
   for (int i = 0; i < KDMA; ++i) {
     const int key = (i * NWL + wu) * KPI + dkey;
+    const int kk = min(key, p.Sk - 1 - kb_last);
     koff[i] = (unsigned)((key * p.k_ss + (dslot ^ (key & (CPR - 1))) * 8) * (int64_t)sizeof(T));
     voff[i] = (unsigned)((key * p.v_ss + (dslot ^ vswz<D>(key)) * 8) * (int64_t)sizeof(T));
+    koffl[i] = (unsigned)((kk * p.k_ss + (dslot ^ (key & (CPR - 1))) * 8) * (int64_t)sizeof(T));
+    voffl[i] = (unsigned)((kk * p.v_ss + (dslot ^ vswz<D>(key)) * 8) * (int64_t)sizeof(T));
   }
   // one DMA instruction (i < KDMA) of the tile starting at key t * kKvTile
-  auto tile_load = [&](const T *base, int64_t ss, unsigned off, V8 *dst, int t, int i, bool kswz) {
+  auto tile_load = [&](const T *base, int64_t ss, unsigned off, unsigned off_last, V8 *dst, int t,
+                       int i) {
     const int kb = t * kKvTile;
     const char *tb = (const char *)(base + (int64_t)kb * ss);
     const int key0 = (i * NWL + wu) * KPI;
-    if (kb + kKvTile > p.Sk) {
-      const int key = key0 + dkey, kk = min(key, p.Sk - 1 - kb);
-      const int ch = kswz ? (dslot ^ (key & (CPR - 1))) : (dslot ^ vswz<D>(key));
-      off = (unsigned)((kk * ss + ch * 8) * (int64_t)sizeof(T));
-    }
-    __builtin_amdgcn_global_load_lds((const void *)(tb + off),
+    const unsigned o = kb + kKvTile > p.Sk ? off_last : off;
+    __builtin_amdgcn_global_load_lds((const void *)(tb + o),
                                      (__attribute__((address_space(3))) void *)&dst[key0 * CPR],
                                      16, 0, 0);
   };
@@ -216,9 +220,9 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
   constexpr int NDMA = 2 * KDMA;
   auto dma = [&](int j, int tk, int kbuf, int tv, int vbuf) {
     if (j < KDMA) {
-      if (tk >= 0) tile_load(kp, p.k_ss, koff[j], sm.k[kbuf], tk, j, true);
+      if (tk >= 0) tile_load(kp, p.k_ss, koff[j], koffl[j], sm.k[kbuf], tk, j);
     } else {
-      if (tv >= 0) tile_load(vp, p.v_ss, voff[j - KDMA], sm.v[vbuf], tv, j - KDMA, false);
+      if (tv >= 0) tile_load(vp, p.v_ss, voff[j - KDMA], voffl[j - KDMA], sm.v[vbuf], tv, j - KDMA);
     }
   };
 
@@ -292,34 +296,41 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
       float mt = -INFINITY;
       if (edge) {
         // score register (st, r) holds key kb + 4h + c, c = 32st + 8(r/4) + r%4;
-        // it is kept iff lo <= key <= hi, i.e. c - A <= U unsigned with
-        // A = lo - kb - 4h, U = hi - lo (an empty range gets A = 2^30, U = 0)
+        // it is kept iff lo <= key <= hi, i.e. c in [lo - jb, hi - jb] with
+        // jb = kb + 4h. Per lane one 32-bit mask per st holds the kept c's;
+        // each score then costs a bit extract (0 or -1) and a bit select,
+        // with no VCC round trip
         const int qpos = qi + off;
         int hi = p.Sk - 1;
         if (p.right >= 0) hi = min(hi, qpos + p.right);
         const int lo = p.left >= 0 ? max(qpos - p.left, 0) : 0;
         const int jb = kb + h * 4;
-        unsigned A = (unsigned)(lo - jb), U = (unsigned)(hi - lo);
-        if (hi < lo) A = 1u << 30, U = 0;
+        const int ca = max(lo - jb, 0), cb = min(hi - jb, 63); // kept c: [ca, cb] (empty if ca > cb)
+        const unsigned ninf = __float_as_uint(-INFINITY);
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+        for (int st = 0; st < 2; ++st) {
+          const int l0 = max(ca - 32 * st, 0), h0 = min(cb - 32 * st, 31);
+          const unsigned keep = l0 <= h0 ? ((2u << h0) - 1u) & ~((1u << l0) - 1u) : 0u;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const unsigned c = st * 32 + (r >> 2) * 8 + (r & 3);
-            s[g][st][r] = c - A <= U ? s[g][st][r] : -INFINITY;
+            const unsigned bm = (unsigned)__builtin_amdgcn_sbfe((int)keep, (r >> 2) * 8 + (r & 3), 1);
+            s[g][st][r] = __uint_as_float((__float_as_uint(s[g][st][r]) & bm) | (ninf & ~bm));
           }
+        }
       }
-      // max and sum as trees: a 32-long dependent chain of VALU ops costs
-      // its full latency per step
-      float mx[8];
+      // max and sum as trees (a 32-long dependent chain of VALU ops costs
+      // its full latency per step); the max as chains of three for v_max3
+      auto max3 = [](float a, float b, float c) { return fmaxf(fmaxf(a, b), c); };
+      float m1[11];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        mx[i] = fmaxf(fmaxf(s[g][0][i], s[g][0][i + 8]), fmaxf(s[g][1][i], s[g][1][i + 8]));
-#pragma unroll
-      for (int n = 4; n >= 1; n >>= 1)
-#pragma unroll
-        for (int i = 0; i < n; ++i) mx[i] = fmaxf(mx[i], mx[i + n]);
-      mt = fmaxf(mt, mx[0]);
+      for (int i = 0; i < 10; ++i) {
+        const int a = 3 * i, b = 3 * i + 1, c = 3 * i + 2;
+        m1[i] = max3(s[g][a >> 4][a & 15], s[g][b >> 4][b & 15], s[g][c >> 4][c & 15]);
+      }
+      m1[10] = fmaxf(s[g][1][14], s[g][1][15]);
+      const float m2a = max3(m1[0], m1[1], m1[2]), m2b = max3(m1[3], m1[4], m1[5]);
+      const float m2c = max3(m1[6], m1[7], m1[8]), m2d = fmaxf(m1[9], m1[10]);
+      mt = fmaxf(max3(m2a, m2b, m2c), m2d);
       {
         // the other half of the wave holds the other 4-key groups
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt),
@@ -336,8 +347,6 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
       const float alpha = move ? __builtin_amdgcn_exp2f(m_run[g] * c2 - mc) : 1.f;
       float ps[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ps[i] = 0.f;
-#pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -345,7 +354,8 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
           if (g == 0 && (st * 16 + r) % kStride == 0) issue((st * 16 + r) / kStride);
           const float e = __builtin_amdgcn_exp2f(fmaf(s[g][st][r], c2, -mc));
           s[g][st][r] = e;
-          ps[r & 7] += e;
+          // the first term of each partial sum starts it (0 + e == e)
+          ps[r & 7] = (st == 0 && r < 8) ? e : ps[r & 7] + e;
         }
 #pragma unroll
       for (int n = 4; n >= 1; n >>= 1)
