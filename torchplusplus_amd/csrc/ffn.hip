@@ -140,8 +140,24 @@ __global__ __launch_bounds__(256) void ffn_decode_kernel(FfnArgs a) {
   const int64_t grow = (int64_t)(c0 / 32) * 64 + (c0 % 32); // first gate row; up rows +32
   V8 *gslot = s_gu + w * (2 * 16 * 32);
   V8 *dslot = s_dn + w * (32 * U2);
-  V8 xa[kFfnNS1], nwv[kFfnNS1];
+  // the down-projection slice by LDS-DMA (every workgroup has one); issued
+  // after the phase-1 loads so that counted waits can take those first
+  auto issue_down = [&]() {
+#pragma unroll
+    for (int jj = 0; jj < U2 / 2; ++jj) {
+      const int q = jj * 64 + lane; // LDS unit: row q / U2, K unit q % U2
+      const int row = q / U2, unit = q % U2;
+      const T *src = Wd + (int64_t)(kFfnRows2 * j + row) * I + x * IX + w * KW2 + unit * 8;
+      __builtin_amdgcn_global_load_lds(
+          (const void *)src, (__attribute__((address_space(3))) void *)(dslot + jj * 64), 16, 0,
+          kCpolNT);
+    }
+  };
+  // The workgroups with a phase-1 tile run their loads, DMA, waits and phase 1
+  // in one branch (the others only issue the down slice), so no branch on
+  // `active1` separates the inline-asm loads from their wait.
   if (active1) {
+    V8 xa[kFfnNS1], nwv[kFfnNS1];
     const bool xok = r < NB;
     const T *xr = resid + (xok ? r : 0) * kFfnE;
 #pragma unroll
@@ -165,20 +181,10 @@ __global__ __launch_bounds__(256) void ffn_decode_kernel(FfnArgs a) {
             (__attribute__((address_space(3))) void *)(gslot + set * 512 + jj * 64), 16, 0,
             kCpolNT);
       }
-  }
-#pragma unroll
-  for (int jj = 0; jj < U2 / 2; ++jj) {
-    const int q = jj * 64 + lane; // LDS unit: row q / U2, K unit q % U2
-    const int row = q / U2, unit = q % U2;
-    const T *src = Wd + (int64_t)(kFfnRows2 * j + row) * I + x * IX + w * KW2 + unit * 8;
-    __builtin_amdgcn_global_load_lds(
-        (const void *)src, (__attribute__((address_space(3))) void *)(dslot + jj * 64), 16, 0,
-        kCpolNT);
-  }
-  __builtin_amdgcn_sched_barrier(0);
+    issue_down();
+    __builtin_amdgcn_sched_barrier(0);
 
-  // ---- phase 1: RMSNorm + gate/up + SwiGLU of this tile -------------------
-  if (active1) {
+    // ---- phase 1: RMSNorm + gate/up + SwiGLU of this tile -----------------
     ffn_vm_wait_tied<16 + U2 / 2>(xa, nwv); // input in; both weight DMAs in flight
     float ss = 0.f;
 #pragma unroll
@@ -237,6 +243,8 @@ __global__ __launch_bounds__(256) void ffn_decode_kernel(FfnArgs a) {
         if (b < NB) H[(int64_t)b * I + c0 + r] = from_f32<T>(s * ut);
       }
     }
+  } else {
+    issue_down();
   }
 
   // ---- XCD-local sync -------------------------------------------------------
