@@ -62,6 +62,32 @@ def test_linear_pipelined_strided_output(dev):
     assert torch.count_nonzero(out[:, 2048:]) == 0
 
 
+@pytest.mark.parametrize("m,n,k,dtype", [(5900, 4100, 128, torch.bfloat16), (8900, 2700, 64, torch.float16),
+                                         (16384, 2048, 320, torch.bfloat16)])
+def test_linear_persistent_path(dev, m, n, k, dtype):
+    """256x256-tile launches with more tiles than CUs run one workgroup per CU
+    over its tiles, the K steps of consecutive tiles in one DMA stream:
+    ragged M and N (element-wise tail stores), one K step per tile (K = 64),
+    and blocks with 1, 2 and 2+ tiles."""
+    x, w, _ = _mk(m, n, k, dtype, seed=23, wstd=0.05)
+    y = ext().linear(x.to(dev), w.to(dev), None, ACTS["none"])
+    close(y, oracle.linear_act(x, w, None, "none"), what=f"persistent {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("rows,inter,k", [(5200, 2400, 192), (16384, 3072, 128)])
+def test_swiglu_persistent_path(dev, rows, inter, k):
+    """SwiGLU through the persistent 256x256 kernel: ragged rows and [gate|up]
+    pairs past the last full tile."""
+    g = torch.Generator().manual_seed(24)
+    x = torch.randn(rows, k, generator=g).bfloat16()
+    wg = (0.05 * torch.randn(inter, k, generator=g)).bfloat16()
+    wu = (0.05 * torch.randn(inter, k, generator=g)).bfloat16()
+    y = L.swiglu(x.to(dev), L.interleave_gate_up(wg, wu).to(dev))
+    gt = oracle.linear_act(x, wg)
+    e = (torch.nn.functional.silu(gt.float()).bfloat16().float() * oracle.linear_act(x, wu).float()).bfloat16()
+    close(y, e, what=f"swiglu persistent {rows}x{inter}x{k}")
+
+
 def test_linear_odd_k_scalar_path(dev):
     x, w, b = _mk(33, 40, 13, torch.float16, seed=2, wstd=0.2)
     y = ext().linear(x.to(dev), w.to(dev), None, ACTS["gelu"])
@@ -187,7 +213,8 @@ def test_gemv_argmax_lm_head(dev, bsz, n):
 
 
 @pytest.mark.parametrize("bsz,n,k,norm", [(16, 40001, 512, True), (1, 33000, 256, False),
-                                           (5, 50000, 768, True), (8, 36000, 1024, False)])
+                                           (5, 50000, 768, True), (8, 36000, 1024, False),
+                                           (2, 34000, 256, True)])
 def test_gemv_wide_path(dev, bsz, n, k, norm):
     """>= 2048 row tiles with K % 256 == 0 run the whole-K-per-wave kernel:
     ragged last tile, every chunk count, with and without the input norm."""

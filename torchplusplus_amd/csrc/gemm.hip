@@ -460,6 +460,266 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent 256x256 variant for launches with more tiles than CUs (the
+// prefill projections: 4-6 tiles per CU). One workgroup per CU loops over the
+// tiles b, b + gridDim, ... (all on the workgroup's XCD: gridDim is a
+// multiple of 8, and tile_coords keeps an XCD's tiles a compact group). The
+// K steps of consecutive tiles form one stream through the 2-stage ring: the
+// last K step of a tile issues the DMA of the next tile's first K step, and
+// the epilogue, staged through the slot that K step has just finished
+// reading (64 KB: 8 KB per wave, two passes), issues the next tile's second
+// K step before its global stores, so neither the first DMA of a tile nor the
+// store drain sits on the critical path. Measured on the prefill shapes:
+// 3-7% faster than one workgroup per tile. Plain and SwiGLU epilogues only
+// (a bias prefetch for the next tile does not fit the registers).
+template <typename T, int EPI, int ACT>
+__global__ __launch_bounds__(512) void gemm_persist_kernel(
+    const T *__restrict__ A, int64_t lda, const T *__restrict__ B, int64_t ldb,
+    T *__restrict__ C, int64_t ldc, const T *__restrict__ bias, int M, int N, int K) {
+  typedef typename VecT<T>::v8 V8;
+  typedef typename VecT<T>::v4 V4;
+  static_assert(EPI == kGPlain || EPI == kGSwiGLU, "plain or SwiGLU epilogue");
+  constexpr int FM = 2, FN = 4, WM = 4, WN = 2, BK = 64, NST = 2;
+  constexpr int BM = 32 * WM * FM, BN = 32 * WN * FN, NWV = WM * WN;
+  constexpr int CPR = BK / 8, RPI = 64 / CPR;
+  constexpr int STG = (BM + BN) * CPR;
+  constexpr int NA = BM / RPI / NWV, NB = BN / RPI / NWV, NQ = NA + NB;
+  constexpr int KS = BK / 16, NMF = KS * FM * FN, MID = NMF - (FM * FN) / 2;
+  constexpr int SP = (NMF / 2) / NQ > 0 ? (NMF / 2) / NQ : 1;
+  static_assert(NQ * SP <= MID, "all DMA of a K step issued before its barrier");
+  // epilogue staging per wave and pass: 64 rows x OWP output columns, read
+  // back in NR rounds of 16 bytes per lane (NSTO global stores per wave)
+  constexpr int OWP = (EPI == kGSwiGLU) ? 32 : 64;
+  constexpr int RB = OWP * (int)sizeof(T), LPR = RB / 16, OPR = 64 / LPR;
+  constexpr int NR = FM * 32 / OPR, NSTO = 2 * NR;
+  static_assert(NWV * FM * 32 * RB <= STG * 16, "staging fits one ring slot");
+  __shared__ V8 smem[NST * STG];
+
+  const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN, ntiles = ntm * ntn;
+  // wave index in a scalar register: every per-wave decision (DMA rows,
+  // store path, wait counts) is then provably uniform
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w / WN, wn = w % WN;
+  const int half = lane >> 5, ml = lane & 31;
+  const int lrow = lane / CPR, lkc = (lane % CPR) ^ swzk<BK>(RPI * w + lrow);
+  const int nk = K / BK;
+  int tile = blockIdx.x;
+  if (tile >= ntiles) return;
+
+  // DMA sources of a tile: uniform tile bases plus per-lane 32-bit offsets of
+  // the lane's clamped rows (the host keeps BM * ld * sizeof(T) below 2^32)
+  struct Src {
+    const char *ta, *tb;
+    uint32_t off[NQ];
+    int m0, n0;
+  };
+  auto src_of = [&](int t, Src &s) {
+    int tm, tn;
+    tile_coords(t, ntiles, ntm, ntn, tm, tn);
+    s.m0 = tm * BM;
+    s.n0 = tn * BN;
+    s.ta = reinterpret_cast<const char *>(A) + (int64_t)s.m0 * lda * (int64_t)sizeof(T);
+    s.tb = reinterpret_cast<const char *>(B) + (int64_t)s.n0 * ldb * (int64_t)sizeof(T);
+#pragma unroll
+    for (int q = 0; q < NA; ++q)
+      s.off[q] = (uint32_t)((int64_t)(min(s.m0 + w * RPI + lrow + RPI * NWV * q, M - 1) - s.m0) * lda +
+                            lkc * 8) * (uint32_t)sizeof(T);
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+      s.off[NA + q] = (uint32_t)((int64_t)(min(s.n0 + w * RPI + lrow + RPI * NWV * q, N - 1) - s.n0) * ldb +
+                                 lkc * 8) * (uint32_t)sizeof(T);
+  };
+  auto issue = [&](const Src &s, int stage, int kt, int q) {
+    V8 *sa = smem + stage * STG, *sb = sa + BM * CPR;
+    const int64_t kb = (int64_t)kt * BK * sizeof(T);
+    if (q < NA)
+      __builtin_amdgcn_global_load_lds((const void *)(s.ta + kb + s.off[q]),
+                                       (__attribute__((address_space(3))) void *)(sa + (q * NWV + w) * 64),
+                                       16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds((const void *)(s.tb + kb + s.off[q]),
+                                       (__attribute__((address_space(3))) void *)(sb + ((q - NA) * NWV + w) * 64),
+                                       16, 0, 0);
+  };
+  V8 af[2][FM], bfr[2][FN];
+  auto frag = [&](const V8 *sa, int ks) {
+    const V8 *sb = sa + BM * CPR;
+    const int kc = ks * 2 + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int row = wm * FM * 32 + i * 32 + (lane & 31);
+      af[ks & 1][i] = sa[row * CPR + (kc ^ swzk<BK>(row))];
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = wn * FN * 32 + j * 32 + (lane & 31);
+      bfr[ks & 1][j] = sb[col * CPR + (kc ^ swzk<BK>(col))];
+    }
+  };
+
+  Src cur, nxt;
+  src_of(tile, cur);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) issue(cur, 0, 0, q);
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  frag(smem, 0);
+  int slot = 0;
+  // K step 1 of the current tile already in flight (issued in the previous
+  // tile's epilogue), with `sto` store instructions of that epilogue issued
+  // after it (-1: an unknown number)
+  bool pre = false;
+  int sto = -1;
+  for (;;) {
+    const int tnext = tile + (int)gridDim.x;
+    const bool has_next = tnext < ntiles;
+    if (has_next) src_of(tnext, nxt);
+    const int nw0 = cur.n0 + wn * FN * 32; // first W row (output column before SwiGLU) of the wave
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // K loop: step kt reads slot `slot`; its DMA fills the other slot with
+    // K step kt + 1, or with the next tile's first K step after the last
+    for (int kt = 0; kt < nk; ++kt) {
+      const V8 *sa = smem + slot * STG;
+      const bool last = kt + 1 == nk;
+      const bool more = !last || has_next;
+      const bool early = kt == 0 && pre; // this step's DMA was issued early
+      const bool dma = more && !early;
+      const Src &ds = last ? nxt : cur;
+      const int kd = last ? 0 : kt + 1;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) frag(sa, ks + 1);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            acc[i][j] = mfma32<T>(bfr[ks & 1][j], af[ks & 1][i], acc[i][j]);
+            const int m = (ks * FM + i) * FN + j + 1;
+            if (m % SP == 0 && m / SP <= NQ && dma) issue(ds, slot ^ 1, kd, m / SP - 1);
+            if (m == MID && more) {
+              // the other slot's DMA landed; this slot's fragment reads all
+              // returned (the MFMAs above consumed them). Vector memory
+              // operations complete in issue order, so behind an early DMA
+              // only the epilogue stores issued after it may stay in flight.
+              if (early && sto == NSTO) wait_vmcnt<NSTO>();
+              else wait_vmcnt<0>();
+              __builtin_amdgcn_s_barrier();
+              frag(smem + (slot ^ 1) * STG, 0);
+            }
+          }
+      }
+      slot ^= 1;
+    }
+
+    // Epilogue through the slot the last K step read (slot ^ 1 now), which
+    // every wave has finished with after this barrier; the next tile's first
+    // K step is in the other slot (its first fragments already requested).
+    // The output is converted, staged (per wave, two passes of OWP columns)
+    // and read back into registers; then the next tile's second K step is
+    // issued into the staging slot ahead of the global stores, so the stores
+    // drain under the next tile's first K step.
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    T *stage = reinterpret_cast<T *>(smem + (slot ^ 1) * STG) + w * (FM * 32 * OWP);
+    auto sw = [](int row) { return (RB == 128) ? (row >> 1) & 7 : (row >> 2) & 3; };
+    const int NO = (EPI == kGSwiGLU) ? N / 2 : N;
+    const int oc0 = (EPI == kGSwiGLU) ? nw0 / 2 : nw0;
+    V8 ov[2][NR];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * p + jj;
+        if constexpr (EPI == kGSwiGLU) {
+          if (jj == 1) continue;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            V4 pk;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float v = acc[i][j][4 * q + e];
+              if constexpr (EPI == kGSwiGLU) {
+                const float gt = to_f32(from_f32<T>(v));
+                const float sl = to_f32(from_f32<T>(act_silu(gt)));
+                v = sl * to_f32(from_f32<T>(acc[i][j + 1][4 * q + e]));
+              }
+              pk[e] = from_f32<T>(v);
+            }
+            const int row = i * 32 + ml;
+            const int col = ((EPI == kGSwiGLU) ? 0 : jj * 32) + q * 8 + half * 4; // column in the pass
+            const int byte = row * RB + (((col * (int)sizeof(T)) / 16) ^ sw(row)) * 16 +
+                             (col * (int)sizeof(T)) % 16;
+            *reinterpret_cast<V4 *>(reinterpret_cast<char *>(stage) + byte) = pk;
+          }
+        }
+      }
+      wait_lgkmcnt0(); // this wave's staging rows written (the staging is per wave)
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int rl = r * OPR + lane / LPR, ch = lane % LPR;
+        ov[p][r] = *reinterpret_cast<const V8 *>(reinterpret_cast<const char *>(stage) + rl * RB +
+                                                 (ch ^ sw(rl)) * 16);
+      }
+      wait_lgkmcnt0(); // the staging reads returned before the next pass overwrites it
+    }
+    // every wave is done with the staging slot: the next tile's second K step
+    // may refill it
+    __builtin_amdgcn_s_barrier();
+    pre = has_next && nk > 1;
+    if (pre) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) issue(nxt, slot ^ 1, 1, q);
+    }
+    __builtin_amdgcn_sched_barrier(0); // the stores stay behind the DMA
+    const int orow0 = cur.m0 + wm * FM * 32;
+    const bool vec_ok = (ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+    // whole wave tile inside the output: one 16-byte store per readback round
+    const bool full = vec_ok && orow0 + FM * 32 <= M && oc0 + 2 * OWP <= NO;
+    if (full) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const int rl = r * OPR + lane / LPR, ch = lane % LPR;
+          *reinterpret_cast<V8 *>(C + (int64_t)(orow0 + rl) * ldc + oc0 + p * OWP + ch * 8) = ov[p][r];
+        }
+    } else {
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const int rl = r * OPR + lane / LPR, ch = lane % LPR;
+          const int row = orow0 + rl;
+          const int col = oc0 + p * OWP + ch * 8;
+          if (row >= M) continue;
+          T *dst = C + (int64_t)row * ldc + col;
+          if (vec_ok && col + 8 <= NO) {
+            *reinterpret_cast<V8 *>(dst) = ov[p][r];
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (col + e < NO) dst[e] = ov[p][r][e];
+          }
+        }
+    }
+    sto = full ? NSTO : -1;
+    if (!has_next) break;
+    tile = tnext;
+    cur = nxt;
+  }
+}
+
 // Tile shape for the DMA kernel: minimise (tiles per CU, rounded up) x tile
 // area / relative efficiency (one block per CU for every candidate). SwiGLU
 // needs whole [gate|up] 64-column pairs per wave (FN even).
@@ -550,7 +810,21 @@ static int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, v
     case 0: launch_dma<T, EPI, ACT, 1, 2, 4, 2, kSmallBK, kSmallNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
     case 1: launch_dma<T, EPI, ACT, 1, 3, 4, 2, kSmallBK, kSmallNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
     case 2: launch_dma<T, EPI, ACT, 1, 4, 4, 2, kSmallBK, kSmallNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    default: launch_dma<T, EPI, ACT, 2, 4, 4, 2, kBigBK, kBigNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    default: {
+      // more tiles than CUs: the persistent kernel (plain / SwiGLU epilogue)
+      bool done = false;
+      if constexpr (EPI != kGBiasAct && kBigBK == 64 && kBigNST == 2) {
+        const int cus = device_cus();
+        const int64_t nb = ((M + 255) / 256) * ((N + 255) / 256);
+        if (cus % 8 == 0 && nb > cus) {
+          gemm_persist_kernel<T, EPI, ACT><<<dim3((unsigned)cus), dim3(512), 0, st>>>(
+              (const T *)A, lda, (const T *)B, ldb, (T *)C, ldc, (const T *)bias, (int)M, (int)N, (int)K);
+          done = true;
+        }
+      }
+      if (!done) launch_dma<T, EPI, ACT, 2, 4, 4, 2, kBigBK, kBigNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st);
+      break;
+    }
     }
   } else if (vec) {
     const int64_t nb = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
