@@ -470,14 +470,24 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
   if (t_begin < t_end) pv((t_end - 1 - t_begin) & 1);
   if (lead) bar();
 
+  // Epilogue: each wave stages its 32 x D output rows in LDS (8 KB for
+  // D = 128; the leading group in the K slots, free once it passes the
+  // barrier above, the trailing group in the V slots after one more barrier
+  // that ends every wave's last PV), then stores whole 16-byte chunks, D / 8
+  // lanes per output row. Straight from the accumulators each store would
+  // write 8 bytes into each of 32 rows: 4x the write requests.
   typedef typename VecT<T>::v4 V4;
+  constexpr int RBY = D * (int)sizeof(T), OCH = RBY / 16, ORPI = 64 / OCH; // row bytes, chunks, rows per pass
+  static_assert(NWL * 32 * RBY <= (int)sizeof(sm.k) && NWL * 32 * RBY <= (int)sizeof(sm.v),
+                "a group's staging fits its slots");
+  if (!lead) bar();
+  char *stg = reinterpret_cast<char *>(lead ? &sm.k[0][0] : &sm.v[0][0]) + wu * (32 * RBY);
 #pragma unroll
   for (int g = 0; g < QG; ++g) {
     const float l = l_run[g] + __shfl_xor(l_run[g], 32, kWave);
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int qi = qw + g * 32 + ql;
-    if (qi >= p.Sq) continue;
-    T *op = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)qi * p.o_ss + (int64_t)hq * p.o_sh;
+    // register 4rg..4rg+3 of tile tt: dims tt*32 + rg*8 + h*4 + 0..3 of query ql,
+    // i.e. half h of 16-byte chunk tt*4 + rg of row ql (chunks XOR-swizzled by row)
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
@@ -485,9 +495,20 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
         V4 pk;
 #pragma unroll
         for (int i = 0; i < 4; ++i) pk[i] = from_f32<T>(o[g][tt][rg * 4 + i] * inv);
-        *reinterpret_cast<V4 *>(op + tt * 32 + rg * 8 + h * 4) = pk;
+        const int ch = (tt * 4 + rg) ^ (ql % OCH);
+        *reinterpret_cast<V4 *>(stg + ql * RBY + ch * 16 + h * 8) = pk;
       }
+#pragma unroll
+    for (int r0 = 0; r0 < 32; r0 += ORPI) {
+      const int row = r0 + lane / OCH, c = lane % OCH;
+      const V8 v = *reinterpret_cast<const V8 *>(stg + row * RBY + ((c ^ (row % OCH)) * 16));
+      const int qi = qw + g * 32 + row;
+      if (qi < p.Sq)
+        *reinterpret_cast<V8 *>((T *)p.o + (int64_t)b * p.o_sb + (int64_t)qi * p.o_ss +
+                                (int64_t)hq * p.o_sh + c * 8) = v;
+    }
   }
+  if (lead) bar();
 }
 
 // Generic prefill (any D <= 256, any alignment): one wave per (b, query,
