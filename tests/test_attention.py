@@ -52,6 +52,21 @@ def test_prefill_shapes(dev, dtype, b, sq, sk, hq, hkv, d, causal, window):
     close(o, oracle.attention(q, k, v, causal=causal, window=window), what="prefill")
 
 
+@pytest.mark.parametrize("b,sq,sk,hq,hkv,d,window", [
+    (8, 1500, 1530, 8, 4, 64, (-1, -1)),   # 384 items, pairs split over the XCDs, Sq < Sk
+    (8, 1500, 1530, 8, 4, 64, (200, 0)),   # same with a window (items of unequal length)
+    (5, 1100, 1100, 12, 4, 64, (-1, -1)),  # 300 items, 60 pairs: round-robin items, G = 3
+    (5, 1100, 1100, 12, 4, 64, (300, 0)),
+])
+def test_prefill_persistent_items(dev, b, sq, sk, hq, hkv, d, window):
+    """More work items (query tile x batch x head group) than CUs: each
+    workgroup runs several, the next item's q rows and first K / V tiles
+    requested during the previous item's epilogue."""
+    q, k, v = _qkv(b, sq, sk, hq, hkv, d, torch.bfloat16, seed=6)
+    o = flash_attn_func(q.to(dev), k.to(dev), v.to(dev), causal=True, window_size=window)
+    close(o, oracle.attention(q, k, v, causal=True, window=window), what=f"persistent window={window}")
+
+
 @pytest.mark.parametrize("d", [32, 96])
 def test_prefill_generic_head_dims(dev, d):
     q, k, v = _qkv(1, 37, 37, 4, 2, d, torch.bfloat16, seed=2)

@@ -116,42 +116,62 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
   const int nqt = (p.Sq + qt_len - 1) / qt_len;
   const int nhg = p.Hq / hpb;
   const int npair = p.B * nhg;
-  int qt, rest;
-  if (npair % 8 == 0) {
-    // workgroups are dealt to the 8 XCDs round-robin (XCD = blockIdx % 8):
-    // each XCD gets whole (batch, head group) pairs, so the K / V tiles its
-    // blocks share stay in its own L2; heavy (late) query tiles start first
-    const int per = npair / 8, j = blockIdx.x / 8;
-    rest = (blockIdx.x % 8) * per + j % per;
-    qt = nqt - 1 - j / per;
-  } else {
-    qt = nqt - 1 - blockIdx.x / npair;
-    rest = blockIdx.x % npair;
-  }
-  const int b = rest / nhg, hg = rest % nhg;
-  const int hq = hg * hpb + w / wph;
-  const int hk = (hg * hpb) / G;
-  const int q0 = qt * qt_len;
-  const int q_last = (q0 + qt_len < p.Sq ? q0 + qt_len : p.Sq) - 1;
-  const int qw = q0 + (w % wph) * 32 * QG; // first query of this wave
+  const int nitems = npair * nqt;
   const int off = p.Sk - p.Sq;
 
-  // key band of the whole block
-  int hi = p.Sk, lo = 0;
-  if (p.right >= 0) {
-    const int lim = q_last + off + p.right + 1;
-    hi = lim < hi ? lim : hi;
-  }
-  if (p.left >= 0) {
-    const int lim = q0 + off - p.left;
-    lo = lim > 0 ? lim : 0;
-  }
-  const int t_begin = lo / kKvTile;
-  const int t_end = hi > lo ? (hi + kKvTile - 1) / kKvTile : t_begin;
-
-  const T *qp = (const T *)p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh;
-  const T *kp = (const T *)p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-  const T *vp = (const T *)p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
+  // Work items (query tile qt, batch x head-group pair) in a fixed order,
+  // heavy (late) query tiles first; the block loops over its share of them.
+  // When the pairs split evenly over the 8 XCDs (workgroups are dealt to
+  // them round-robin, XCD = blockIdx % 8), an XCD runs only its own pairs,
+  // so the K / V tiles its blocks share stay in its L2, and each of its S
+  // blocks takes the XCD's items in boustrophedon order (rounds alternate
+  // direction), which evens out the heavy and light tiles per block.
+  const bool xcd_split = npair % 8 == 0 && gridDim.x % 8 == 0;
+  auto next_item = [&](int &k, int &qt, int &rest) -> bool {
+    if (xcd_split) {
+      const int S = gridDim.x / 8, slot = blockIdx.x / 8, per = npair / 8, ni = nitems / 8;
+      for (;; ++k) {
+        if (k * S >= ni) return false;
+        const int j = (k & 1) ? (k + 1) * S - 1 - slot : k * S + slot;
+        if (j >= ni) continue;
+        rest = (blockIdx.x % 8) * per + j % per;
+        qt = nqt - 1 - j / per;
+        return true;
+      }
+    }
+    const int it = blockIdx.x + k * gridDim.x;
+    if (it >= nitems) return false;
+    qt = nqt - 1 - it / npair;
+    rest = it % npair;
+    return true;
+  };
+  // the item's state (set by setup)
+  int b, hq, hk, q0, q_last, qw, t_begin, t_end;
+  const T *qp, *kp, *vp;
+  auto setup = [&](int qt, int rest) {
+    b = rest / nhg;
+    const int hg = rest % nhg;
+    hq = hg * hpb + w / wph;
+    hk = (hg * hpb) / G;
+    q0 = qt * qt_len;
+    q_last = (q0 + qt_len < p.Sq ? q0 + qt_len : p.Sq) - 1;
+    qw = q0 + (w % wph) * 32 * QG; // first query of this wave
+    // key band of the whole item
+    int hi = p.Sk, lo = 0;
+    if (p.right >= 0) {
+      const int lim = q_last + off + p.right + 1;
+      hi = lim < hi ? lim : hi;
+    }
+    if (p.left >= 0) {
+      const int lim = q0 + off - p.left;
+      lo = lim > 0 ? lim : 0;
+    }
+    t_begin = lo / kKvTile;
+    t_end = hi > lo ? (hi + kKvTile - 1) / kKvTile : t_begin;
+    qp = (const T *)p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh;
+    kp = (const T *)p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+    vp = (const T *)p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
+  };
 
   V8 zero;
 #pragma unroll
@@ -159,15 +179,21 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
 
   // QG groups of 32 queries per wave share every K / V fragment read from LDS
   V8 qf[QG][D / 16];
+  auto load_q = [&] {
 #pragma unroll
-  for (int g = 0; g < QG; ++g) {
-    const int qi = qw + g * 32 + ql;
+    for (int g = 0; g < QG; ++g) {
+      const int qi = qw + g * 32 + ql;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
-      qf[g][ks] = qi < p.Sq
-                      ? *reinterpret_cast<const V8 *>(qp + (int64_t)qi * p.q_ss + ks * 16 + h * 8)
-                      : zero;
-  }
+      for (int ks = 0; ks < D / 16; ++ks)
+        qf[g][ks] = qi < p.Sq
+                        ? *reinterpret_cast<const V8 *>(qp + (int64_t)qi * p.q_ss + ks * 16 + h * 8)
+                        : zero;
+    }
+  };
+  int kitem = 0, qt0, rest0;
+  if (!next_item(kitem, qt0, rest0)) return;
+  setup(qt0, rest0);
+  load_q();
 
   // The block's waves form two groups of NW/2 (waves w and w + NW/2 share a
   // SIMD). The leading group runs half an iteration ahead of the trailing
@@ -226,16 +252,8 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
     }
   };
 
-  f32x16 o[QG][NT];
-#pragma unroll
-  for (int g = 0; g < QG; ++g)
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[g][t][r] = 0.f;
+  f32x16 o[QG][NT];                // reset at the start of every item
   float m_run[QG], l_run[QG];
-#pragma unroll
-  for (int g = 0; g < QG; ++g) m_run[g] = -INFINITY, l_run[g] = 0.f;
 
   f32x16 s[QG][2];
   V8 pb[QG][4];
@@ -446,69 +464,102 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  if (t_begin < t_end) {
+  // K(t_begin), K(t_begin + 1), V(t_begin) of the item, into slots 0 / 1 / 0
+  auto first_dma = [&] {
+    if (t_begin < t_end) {
 #pragma unroll
-    for (int j = 0; j < NDMA; ++j) {
-      if (lead) dma(j, j < KDMA ? t_begin : -1, 0, -1, 0);
-      else dma(j, t_begin + 1 < t_end ? t_begin + 1 : -1, 1, t_begin, 0);
+      for (int j = 0; j < NDMA; ++j) {
+        if (lead) dma(j, j < KDMA ? t_begin : -1, 0, -1, 0);
+        else dma(j, t_begin + 1 < t_end ? t_begin + 1 : -1, 1, t_begin, 0);
+      }
     }
-  }
-  __syncthreads(); // (its fence also drains the DMA)
-  if (!lead) bar();
-  for (int t = t_begin; t < t_end; ++t) {
-    const int buf = (t - t_begin) & 1;
-    if (t > t_begin) pv(buf ^ 1);
-    qk(buf);
-    if (!lead) __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): K(t+1), V(t) landed
-    bar();
-    const int tk = t + 2 < t_end ? t + 2 : -1, tv = t + 1 < t_end ? t + 1 : -1;
-    softmax(t, [&](int j) {
-      if (!lead) dma(j, tk, buf, tv, buf ^ 1);
-    });
-    bar();
-  }
-  if (t_begin < t_end) pv((t_end - 1 - t_begin) & 1);
-  if (lead) bar();
-
-  // Epilogue: each wave stages its 32 x D output rows in LDS (8 KB for
-  // D = 128; the leading group in the K slots, free once it passes the
-  // barrier above, the trailing group in the V slots after one more barrier
-  // that ends every wave's last PV), then stores whole 16-byte chunks, D / 8
-  // lanes per output row. Straight from the accumulators each store would
-  // write 8 bytes into each of 32 rows: 4x the write requests.
+  };
+  // Output staging, 32 rows x D per wave, apart from the K / V slots so the
+  // next item's first tiles can land while this item's rows are written out
   typedef typename VecT<T>::v4 V4;
   constexpr int RBY = D * (int)sizeof(T), OCH = RBY / 16, ORPI = 64 / OCH; // row bytes, chunks, rows per pass
-  static_assert(NWL * 32 * RBY <= (int)sizeof(sm.k) && NWL * 32 * RBY <= (int)sizeof(sm.v),
-                "a group's staging fits its slots");
-  if (!lead) bar();
-  char *stg = reinterpret_cast<char *>(lead ? &sm.k[0][0] : &sm.v[0][0]) + wu * (32 * RBY);
+  __shared__ V8 stage_all[NW * 32 * OCH];
+  char *const stg = reinterpret_cast<char *>(stage_all) + w * (32 * RBY);
+
+  first_dma();
+  for (;;) {
+    __syncthreads(); // (its fence also drains the DMA and the q loads)
 #pragma unroll
-  for (int g = 0; g < QG; ++g) {
-    const float l = l_run[g] + __shfl_xor(l_run[g], 32, kWave);
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    // register 4rg..4rg+3 of tile tt: dims tt*32 + rg*8 + h*4 + 0..3 of query ql,
-    // i.e. half h of 16-byte chunk tt*4 + rg of row ql (chunks XOR-swizzled by row)
+    for (int g = 0; g < QG; ++g) {
+      m_run[g] = -INFINITY, l_run[g] = 0.f;
 #pragma unroll
-    for (int tt = 0; tt < NT; ++tt)
+      for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        V4 pk;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pk[i] = from_f32<T>(o[g][tt][rg * 4 + i] * inv);
-        const int ch = (tt * 4 + rg) ^ (ql % OCH);
-        *reinterpret_cast<V4 *>(stg + ql * RBY + ch * 16 + h * 8) = pk;
-      }
-#pragma unroll
-    for (int r0 = 0; r0 < 32; r0 += ORPI) {
-      const int row = r0 + lane / OCH, c = lane % OCH;
-      const V8 v = *reinterpret_cast<const V8 *>(stg + row * RBY + ((c ^ (row % OCH)) * 16));
-      const int qi = qw + g * 32 + row;
-      if (qi < p.Sq)
-        *reinterpret_cast<V8 *>((T *)p.o + (int64_t)b * p.o_sb + (int64_t)qi * p.o_ss +
-                                (int64_t)hq * p.o_sh + c * 8) = v;
+        for (int r = 0; r < 16; ++r) o[g][tt][r] = 0.f;
     }
+    if (!lead) bar();
+    for (int t = t_begin; t < t_end; ++t) {
+      const int buf = (t - t_begin) & 1;
+      if (t > t_begin) pv(buf ^ 1);
+      qk(buf);
+      if (!lead) __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): K(t+1), V(t) landed
+      bar();
+      const int tk = t + 2 < t_end ? t + 2 : -1, tv = t + 1 < t_end ? t + 1 : -1;
+      softmax(t, [&](int j) {
+        if (!lead) dma(j, tk, buf, tv, buf ^ 1);
+      });
+      bar();
+    }
+    if (t_begin < t_end) pv((t_end - 1 - t_begin) & 1);
+    if (lead) bar();
+
+    // The item's output rows, then the next item: its q rows are requested
+    // now (q is dead after the last QK^T), its first K / V tiles once every
+    // wave is past its last PV (the barrier below), after the staging reads.
+    const int oqw = qw;
+    T *const orow = (T *)p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
+    int qt1 = 0, rest1 = 0;
+    ++kitem;
+    const bool more = next_item(kitem, qt1, rest1);
+    if (more) {
+      setup(qt1, rest1);
+      load_q();
+    }
+    bar(); // every wave is done with the K / V slots
+
+    // Epilogue: each wave stages its 32 x D output rows in LDS and reads
+    // them back as whole 16-byte chunks, D / 8 lanes per output row (straight
+    // from the accumulators each store would write 8 bytes into each of 32
+    // rows: 4x the write requests).
+#pragma unroll
+    for (int g = 0; g < QG; ++g) {
+      const float l = l_run[g] + __shfl_xor(l_run[g], 32, kWave);
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      // register 4rg..4rg+3 of tile tt: dims tt*32 + rg*8 + h*4 + 0..3 of query ql,
+      // i.e. half h of 16-byte chunk tt*4 + rg of row ql (chunks XOR-swizzled by row)
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          V4 pk;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pk[i] = from_f32<T>(o[g][tt][rg * 4 + i] * inv);
+          const int ch = (tt * 4 + rg) ^ (ql % OCH);
+          *reinterpret_cast<V4 *>(stg + ql * RBY + ch * 16 + h * 8) = pk;
+        }
+      V8 ov[32 / ORPI];
+#pragma unroll
+      for (int r = 0; r < 32 / ORPI; ++r) {
+        const int row = r * ORPI + lane / OCH, c = lane % OCH;
+        ov[r] = *reinterpret_cast<const V8 *>(stg + row * RBY + ((c ^ (row % OCH)) * 16));
+      }
+      // the DMA goes out after the staging reads: an LDS read issued behind
+      // an LDS-DMA waits for it
+      if (g == QG - 1 && more) first_dma();
+#pragma unroll
+      for (int r = 0; r < 32 / ORPI; ++r) {
+        const int row = r * ORPI + lane / OCH, c = lane % OCH;
+        const int qi = oqw + g * 32 + row;
+        if (qi < p.Sq) *reinterpret_cast<V8 *>(orow + (int64_t)qi * p.o_ss + c * 8) = ov[r];
+      }
+    }
+    if (!more) break;
   }
-  if (lead) bar();
 }
 
 // Generic prefill (any D <= 256, any alignment): one wave per (b, query,
@@ -1086,9 +1137,12 @@ static int launch_prefill(const AttnArgs &a, int64_t D, hipStream_t st, const ch
     constexpr int QG = kPrefillQG;
     constexpr int NW = kPrefillWaves;
     const int qt_len = (NW / hpb) * 32 * QG;
-    const int64_t blocks =
+    const int64_t items =
         (int64_t)a.B * (a.Hq / hpb) * ((a.Sq + qt_len - 1) / qt_len);
-    if (blocks > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: too large", name);
+    if (items > 0x7fffffffLL) return set_error(TPP_E_UNSUPPORTED, "%s: too large", name);
+    // one workgroup per CU loops over the work items (more items than CUs)
+    const int cus = device_cu_count();
+    const int64_t blocks = (cus > 0 && items > cus) ? cus : items;
     if (D == 128)
       attn_prefill_kernel<T, 128, QG, NW><<<dim3((unsigned)blocks), dim3(64 * NW), 0, st>>>(a, hpb);
     else

@@ -745,16 +745,8 @@ static int pick_dma_tile(int64_t M, int64_t N, bool swiglu, int cus) {
 }
 
 static int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
+  const int n = device_cu_count();
+  return n > 0 ? n : 256;
 }
 
 template <typename T, int EPI, int ACT, int FM, int FN, int WM, int WN, int BK, int NST>
