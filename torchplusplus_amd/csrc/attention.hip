@@ -95,10 +95,12 @@ template <int D> __device__ __forceinline__ int vswz(int r) {
   else return 4 * ((r >> 1) & 1);
 }
 
+// K / V ring slots of the prefill kernel: tile t in slot (t - t_begin) % 3
+constexpr int kPrefillSlots = 3;
 template <typename T, int D> struct PrefillSmem {
   typedef typename VecT<T>::v8 V8;
-  V8 k[2][kKvTile * D / 8];  // [key][chunk ^ (key % (D/8))]
-  V8 v[2][kKvTile * D / 8];  // [key][chunk ^ vswz(key)]
+  V8 k[kPrefillSlots][kKvTile * D / 8];  // [key][chunk ^ (key % (D/8))]
+  V8 v[kPrefillSlots][kKvTile * D / 8];  // [key][chunk ^ vswz(key)]
 };
 
 template <typename T, int D, int QG, int NW>
@@ -205,51 +207,44 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
   const bool lead = __builtin_amdgcn_readfirstlane(w) < NW / 2; // wave-uniform
   constexpr int NWL = NW / 2;
 
-  // K and V tiles go HBM/L2 -> LDS by LDS-DMA (no staging registers), issued
-  // by one group of NW/2 waves: instruction i of the group's wave w fills 64
-  // slots = 64/CPR keys; lane l fetches the chunk that lands in its slot. The
-  // address is a wave-uniform tile base plus a per-lane 32-bit byte offset
-  // fixed for the whole loop (the launch checks 64 rows fit in 2^31 bytes).
-  // Keys past Sk are clamped to Sk-1 on the last tile (finite data; those
-  // scores are masked, so their P is 0).
+  // K and V tiles go HBM/L2 -> LDS by LDS-DMA (no staging registers): the
+  // leading group fetches the K tiles, the trailing group the V tiles.
+  // Instruction i of a group's wave wu fills 64 slots = 64/CPR keys; lane l
+  // fetches the chunk that lands in its slot. The address is a wave-uniform
+  // tile base plus a per-lane 32-bit byte offset fixed for the whole kernel
+  // (the launch checks 64 rows fit in 2^31 bytes). Keys past Sk are clamped
+  // to Sk-1 on the last tile (finite data; those scores are masked, so their
+  // P is 0).
   constexpr int KPI = 64 / CPR;                 // keys per DMA instruction
   constexpr int KDMA = kKvTile / KPI / NWL;     // DMA instructions per wave per tile
+  constexpr int NDMA = KDMA;                    // ... per wave per iteration
   const int wu = __builtin_amdgcn_readfirstlane(w) % NWL; // wave index within its group
   const int dkey = lane / CPR, dslot = lane % CPR;
+  const int64_t dss = lead ? p.k_ss : p.v_ss; // row stride of this wave's tiles
   // Offsets of full tiles, and of the last tile when Sk is not a multiple of
   // the tile: its keys past Sk read key Sk-1 (the clamp computed here once,
   // not per tile)
   const int kb_last = ((p.Sk - 1) / kKvTile) * kKvTile;
-  unsigned koff[KDMA], voff[KDMA], koffl[KDMA], voffl[KDMA];
+  unsigned doff[KDMA], doffl[KDMA];
 #pragma unroll
   for (int i = 0; i < KDMA; ++i) {
     const int key = (i * NWL + wu) * KPI + dkey;
     const int kk = min(key, p.Sk - 1 - kb_last);
-    koff[i] = (unsigned)((key * p.k_ss + (dslot ^ (key & (CPR - 1))) * 8) * (int64_t)sizeof(T));
-    voff[i] = (unsigned)((key * p.v_ss + (dslot ^ vswz<D>(key)) * 8) * (int64_t)sizeof(T));
-    koffl[i] = (unsigned)((kk * p.k_ss + (dslot ^ (key & (CPR - 1))) * 8) * (int64_t)sizeof(T));
-    voffl[i] = (unsigned)((kk * p.v_ss + (dslot ^ vswz<D>(key)) * 8) * (int64_t)sizeof(T));
+    const int ch = lead ? dslot ^ (key & (CPR - 1)) : dslot ^ vswz<D>(key); // K / V swizzle
+    doff[i] = (unsigned)((key * dss + ch * 8) * (int64_t)sizeof(T));
+    doffl[i] = (unsigned)((kk * dss + ch * 8) * (int64_t)sizeof(T));
   }
-  // one DMA instruction (i < KDMA) of the tile starting at key t * kKvTile
-  auto tile_load = [&](const T *base, int64_t ss, unsigned off, unsigned off_last, V8 *dst, int t,
-                       int i) {
+  // DMA instruction i (< KDMA) of this wave's share of tile t (K tile for the
+  // leading group, V tile for the trailing group) into ring slot `slot`
+  auto dma = [&](int i, int t, int slot) {
     const int kb = t * kKvTile;
-    const char *tb = (const char *)(base + (int64_t)kb * ss);
+    const char *tb = (const char *)((lead ? kp : vp) + (int64_t)kb * dss);
+    V8 *dst = lead ? sm.k[slot] : sm.v[slot];
     const int key0 = (i * NWL + wu) * KPI;
-    const unsigned o = kb + kKvTile > p.Sk ? off_last : off;
+    const unsigned o = kb + kKvTile > p.Sk ? doffl[i] : doff[i];
     __builtin_amdgcn_global_load_lds((const void *)(tb + o),
                                      (__attribute__((address_space(3))) void *)&dst[key0 * CPR],
                                      16, 0, 0);
-  };
-  // DMA instruction j of an iteration: K tile tk (j < KDMA) or V tile tv;
-  // a negative tile index skips it
-  constexpr int NDMA = 2 * KDMA;
-  auto dma = [&](int j, int tk, int kbuf, int tv, int vbuf) {
-    if (j < KDMA) {
-      if (tk >= 0) tile_load(kp, p.k_ss, koff[j], koffl[j], sm.k[kbuf], tk, j);
-    } else {
-      if (tv >= 0) tile_load(vp, p.v_ss, voff[j - KDMA], voffl[j - KDMA], sm.v[vbuf], tv, j - KDMA);
-    }
   };
 
   f32x16 o[QG][NT];                // reset at the start of every item
@@ -301,8 +296,8 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
   // unscaled and exp2(scale*log2e*(s - m)) is one FMA + v_exp_f32 per score
   // (scale > 0 preserves the max). Masking only on band edges.
   // issue(j) is called at evenly spaced points of the exponentials with
-  // j = 0 .. NDMA-1 (the trailing waves put their DMA instructions there: a
-  // burst of them would stall issue on the vector-memory queue)
+  // j = 0 .. NDMA-1 (the waves put their DMA instructions there: a burst of
+  // them would stall issue on the vector-memory queue)
   auto softmax = [&](int t, auto &&issue) {
     const int kb = t * kKvTile;
     const bool edge = (p.right >= 0 && kb + kKvTile - 1 > q0 + off + p.right) ||
@@ -448,15 +443,17 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
     static_for<4>(step);
   };
 
-  // Slots: K tile t and V tile t live in slot (t - t_begin) & 1. The leading
-  // group's MFMA phase of iteration t (PV of V(t-1), QK^T of K(t)) shares its
-  // interval with the trailing group's softmax phase of iteration t-1, in
-  // which the trailing waves request K(t+1) (into the slot of K(t-1)) and
-  // V(t) (into the slot of V(t-2)); both slots were last read in the
-  // trailing group's MFMA phase of iteration t-1, the interval before. They
-  // wait for them at the end of their next MFMA phase, before the barrier
-  // after which the leading group reads them. K(t_begin), K(t_begin+1) and
-  // V(t_begin) are loaded up front.
+  // Slots: K tile t and V tile t live in slot (t - t_begin) % 3. Iteration t
+  // is two intervals: (A) the leading group's MFMA phase (PV of V(t-1),
+  // QK^T of K(t)) beside the trailing group's softmax of tile t-1, then (B)
+  // the leading group's softmax of tile t beside the trailing group's MFMA
+  // phase. Each group requests tiles during its softmax: the leading waves
+  // K(t+2) in (B), into the slot of K(t-1), last read in iteration t-1, and
+  // wait for K(t+1) at the end of it; the trailing waves V(t+1) in (A) of
+  // iteration t+1, into the slot of V(t-2), and wait for it at the end of
+  // their next MFMA phase. Every wait is before the barrier after which the
+  // other group reads the tile. K(t_begin), K(t_begin+1) and V(t_begin) are
+  // loaded up front.
   // barrier without the fence of __syncthreads (which would drain the DMA);
   // the empty asm keeps the compiler from moving LDS accesses across it
   auto bar = [] {
@@ -464,13 +461,15 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  // K(t_begin), K(t_begin + 1), V(t_begin) of the item, into slots 0 / 1 / 0
+  // K(t_begin), K(t_begin + 1) (leading waves), V(t_begin) (trailing waves)
+  // of the item, into slot 0, 1 and 0
   auto first_dma = [&] {
     if (t_begin < t_end) {
 #pragma unroll
-      for (int j = 0; j < NDMA; ++j) {
-        if (lead) dma(j, j < KDMA ? t_begin : -1, 0, -1, 0);
-        else dma(j, t_begin + 1 < t_end ? t_begin + 1 : -1, 1, t_begin, 0);
+      for (int j = 0; j < NDMA; ++j) dma(j, t_begin, 0);
+      if (lead && t_begin + 1 < t_end) {
+#pragma unroll
+        for (int j = 0; j < NDMA; ++j) dma(j, t_begin + 1, 1);
       }
     }
   };
@@ -493,19 +492,31 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnArgs p, int h
         for (int r = 0; r < 16; ++r) o[g][tt][r] = 0.f;
     }
     if (!lead) bar();
+    int sc = 0; // slot of tile t
     for (int t = t_begin; t < t_end; ++t) {
-      const int buf = (t - t_begin) & 1;
-      if (t > t_begin) pv(buf ^ 1);
-      qk(buf);
-      if (!lead) __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): K(t+1), V(t) landed
+      const int sp = sc == 0 ? kPrefillSlots - 1 : sc - 1; // slot of t-1 (and of t+2)
+      const int sn = sc == kPrefillSlots - 1 ? 0 : sc + 1; // slot of t+1
+      if (t > t_begin) pv(sp);
+      qk(sc);
+      if (!lead) __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): V(t) landed
       bar();
-      const int tk = t + 2 < t_end ? t + 2 : -1, tv = t + 1 < t_end ? t + 1 : -1;
+      const bool k2 = t + 2 < t_end;
+      // K(t+2) into the slot of t-1 (leading waves), V(t+1) into the slot of
+      // t+1 (trailing waves)
+      const int dt = lead ? (k2 ? t + 2 : -1) : (t + 1 < t_end ? t + 1 : -1);
+      const int ds = lead ? sp : sn;
       softmax(t, [&](int j) {
-        if (!lead) dma(j, tk, buf, tv, buf ^ 1);
+        if (dt >= 0) dma(j, dt, ds);
       });
+      if (lead) {
+        // K(t+1) landed; K(t+2), issued just now, may stay in flight
+        if (k2) __builtin_amdgcn_s_waitcnt((NDMA & 0xF) | ((NDMA >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+        else __builtin_amdgcn_s_waitcnt(0x0F70);
+      }
       bar();
+      sc = sn;
     }
-    if (t_begin < t_end) pv((t_end - 1 - t_begin) & 1);
+    if (t_begin < t_end) pv(sc == 0 ? kPrefillSlots - 1 : sc - 1);
     if (lead) bar();
 
     // The item's output rows, then the next item: its q rows are requested
