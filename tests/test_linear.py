@@ -45,6 +45,16 @@ def test_linear_pipelined_path_edges(dev, act, m, n):
     close(y, oracle.linear_act(x, w, b, act), what=f"linear {act} {m}x{n}x1024")
 
 
+@pytest.mark.parametrize("m,n", [(2048, 2048), (2048, 3072), (2048, 4096)])
+@pytest.mark.parametrize("k", [64, 128, 192, 256, 320])
+def test_linear_ring_depths_short_k(dev, m, n, k):
+    """128x128 / 128x192 / 128x256 tiles (5-, 4- and 3-stage DMA rings) with
+    fewer K steps than ring stages and every tail of the ring's waits."""
+    x, w, b = _mk(m, n, k, torch.bfloat16, seed=25, wstd=0.05)
+    y = ext().linear(x.to(dev), w.to(dev), b.to(dev), ACTS["silu"])
+    close(y, oracle.linear_act(x, w, b, "silu"), what=f"linear silu {m}x{n}x{k}")
+
+
 def test_linear_pipelined_strided_output(dev):
     """Output rows with a pitch (a column slice of a wider tensor) and K = 3072."""
     x, w, _ = _mk(2048, 2048, 3072, torch.float16, seed=22, wstd=0.02)

@@ -44,14 +44,11 @@ __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 #define TPP_BIG_BK 64
 #define TPP_BIG_NST 2
 #endif
-#ifndef TPP_SMALL_BK
-#define TPP_SMALL_BK 64
-#define TPP_SMALL_NST 3
-#endif
 constexpr int kBigBK = TPP_BIG_BK, kBigNST = TPP_BIG_NST;
-// the same for the 128-row tiles (3 stages: 6% faster than 2 at the
-// Linear+act shape, 96-144 KB, one block per CU)
-constexpr int kSmallBK = TPP_SMALL_BK, kSmallNST = TPP_SMALL_NST;
+// the same for the 128-row tiles: BK 64, as many stages as fit 160 KB of LDS
+// (one block per CU): 5 for 128x128, 4 for 128x192, 3 for 128x256 (at the
+// Linear+act shape 3 stages were 6% faster than 2, and 4 another 3%)
+constexpr int kSmallBK = 64;
 // below this many outputs the register-staged kernel's smaller LDS footprint
 // (several blocks per CU) wins over the deeper DMA ring
 constexpr int64_t kDmaMinMN = 256 * 128 * 128;
@@ -217,6 +214,17 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+// Wait until at most min(later, R) K tiles' DMA (NQ instructions each, this
+// wave's share) are outstanding: the ring's DMA completes in issue order, so
+// every older tile has landed.
+template <int NQ, int R> __device__ __forceinline__ void wait_tiles(int later) {
+  if constexpr (R <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (later >= R) wait_vmcnt<R * NQ>();
+    else wait_tiles<NQ, R - 1>(later);
+  }
+}
 
 template <int BK> __device__ __forceinline__ int swzk(int row) {
   // BK = 64: 128-byte rows, two per 256-byte bank space; BK = 32: 64-byte rows,
@@ -336,10 +344,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
     if (p < nk)
 #pragma unroll
       for (int q = 0; q < NQ; ++q) issue_one(p, p, q);
-  // K tile 0 landed (tile 1 may be in flight)
-  if constexpr (NST == 2) wait_vmcnt<0>();
-  else if (nk > 1) wait_vmcnt<(NST - 2) * NQ>();
-  else wait_vmcnt<0>();
+  // K tile 0 landed (tiles 1 .. NST-2 may be in flight)
+  wait_tiles<NQ, NST - 2>(nk - 1);
   __builtin_amdgcn_s_barrier();
   V8 af[2][FM], bfr[2][FN];
   auto frag = [&](const V8 *sa, int ks) {
@@ -372,13 +378,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
           const int m = (ks * FM + i) * FN + j + 1;
           if (m % SP == 0 && m / SP <= NQ && more) issue_one(kn % NST, kn, m / SP - 1);
           if (m == MID && next) {
-            // own DMA of K tile kt + 1 landed (tile kt + 2's may still be in
-            // flight); the fragment reads of tile kt all returned (the MFMAs
-            // above consumed them), so after the barrier its slot may be
-            // refilled by any wave
-            if constexpr (NST == 2) wait_vmcnt<0>();
-            else if (kt + 2 < nk) wait_vmcnt<(NST - 2) * NQ>();
-            else wait_vmcnt<0>();
+            // own DMA of K tile kt + 1 landed (tiles kt + 2 .. kt + NST - 1
+            // may still be in flight); the fragment reads of tile kt all
+            // returned (the MFMAs above consumed them), so after the barrier
+            // its slot may be refilled by any wave
+            wait_tiles<NQ, NST - 2>(nk - kt - 2);
             __builtin_amdgcn_s_barrier();
             frag(smem + ((kt + 1) % NST) * STG, 0);
           }
@@ -799,9 +803,9 @@ static int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, v
     if ((M + 127) / 128 * ((N + 127) / 128) > 0x7fffffffLL)
       return set_error(TPP_E_UNSUPPORTED, "%s: too many tiles", name);
     switch (pick_dma_tile(M, N, EPI == kGSwiGLU, device_cus())) {
-    case 0: launch_dma<T, EPI, ACT, 1, 2, 4, 2, kSmallBK, kSmallNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    case 1: launch_dma<T, EPI, ACT, 1, 3, 4, 2, kSmallBK, kSmallNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
-    case 2: launch_dma<T, EPI, ACT, 1, 4, 4, 2, kSmallBK, kSmallNST>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 0: launch_dma<T, EPI, ACT, 1, 2, 4, 2, kSmallBK, 5>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 1: launch_dma<T, EPI, ACT, 1, 3, 4, 2, kSmallBK, 4>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
+    case 2: launch_dma<T, EPI, ACT, 1, 4, 4, 2, kSmallBK, 3>(A, lda, B, ldb, C, ldc, bias, M, N, K, st); break;
     default: {
       // more tiles than CUs: the persistent kernel (plain / SwiGLU epilogue)
       bool done = false;
