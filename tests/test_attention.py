@@ -57,6 +57,7 @@ def test_prefill_shapes(dev, dtype, b, sq, sk, hq, hkv, d, causal, window):
     (8, 1500, 1530, 8, 4, 64, (200, 0)),   # same with a window (items of unequal length)
     (5, 1100, 1100, 12, 4, 64, (-1, -1)),  # 300 items, 60 pairs: round-robin items, G = 3
     (5, 1100, 1100, 12, 4, 64, (300, 0)),
+    (4, 2048, 600, 16, 8, 64, (-1, -1)),   # Sq > Sk: items with no visible key between others
 ])
 def test_prefill_persistent_items(dev, b, sq, sk, hq, hkv, d, window):
     """More work items (query tile x batch x head group) than CUs: each
