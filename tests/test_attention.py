@@ -59,11 +59,12 @@ def test_prefill_shapes(dev, dtype, b, sq, sk, hq, hkv, d, causal, window):
     (5, 1100, 1100, 12, 4, 64, (300, 0)),
     (4, 2048, 600, 16, 8, 64, (-1, -1)),   # Sq > Sk: items with no visible key between others
 ])
-def test_prefill_persistent_items(dev, b, sq, sk, hq, hkv, d, window):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_persistent_items(dev, dtype, b, sq, sk, hq, hkv, d, window):
     """More work items (query tile x batch x head group) than CUs: each
     workgroup runs several, the next item's q rows and first K / V tiles
     requested during the previous item's epilogue."""
-    q, k, v = _qkv(b, sq, sk, hq, hkv, d, torch.bfloat16, seed=6)
+    q, k, v = _qkv(b, sq, sk, hq, hkv, d, dtype, seed=6)
     o = flash_attn_func(q.to(dev), k.to(dev), v.to(dev), causal=True, window_size=window)
     close(o, oracle.attention(q, k, v, causal=True, window=window), what=f"persistent window={window}")
 
