@@ -143,3 +143,31 @@ def test_gqa_cached_prefill_then_decode(dev, dtype):
             got = mod(y[:, t:t + 1].to(dev), cd, sd, kv, t)
             close(got, orc2.forward(y[:, t:t + 1], c, s, cache_pos=t),
                   what=f"GQA decode {t}, smaller batch")
+
+
+def test_positions_tensor_reuse(dev):
+    """The [bs] positions tensor the cached GQA path hands to its kernels is
+    reused across layers on one stream, refilled for another value or stream,
+    and never cached from inside a graph capture (its fill would only run at
+    replay)."""
+    from torchplusplus_amd.attention import gqa
+
+    a = gqa._positions(4, 7, dev)
+    assert gqa._positions(4, 7, dev) is a and a.tolist() == [7] * 4
+    assert gqa._positions(4, 8, dev).tolist() == [8] * 4
+    assert gqa._positions(2, 8, dev).tolist() == [8] * 2
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        b = gqa._positions(2, 8, dev)
+    s.synchronize()
+    c = gqa._positions(2, 8, dev)
+    assert b is not c and b.tolist() == c.tolist() == [8] * 2
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        t = gqa._positions(4, 9, dev)
+    e = gqa._positions(4, 9, dev)
+    assert e is not t and e.tolist() == [9] * 4
+    g.replay()
+    torch.cuda.synchronize()
+    assert t.tolist() == [9] * 4

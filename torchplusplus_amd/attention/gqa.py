@@ -24,6 +24,25 @@ from torchplusplus_amd.llmops.kvcache import KVCache
 
 _C = _ext()
 
+# one [bs] int32 positions tensor per device, reused by the layers of a
+# forward pass (one fill launch per pass instead of one per layer)
+_POSITIONS: dict = {}
+
+
+def _positions(bs: int, start: int, dev: torch.device) -> torch.Tensor:
+    """[bs] int32 tensor of `start`, filled on the current stream and reused
+    only on that stream (so its fill is ordered before every kernel that
+    reads it). Not cached while the stream is being captured: a tensor filled
+    inside a capture holds its value only once the graph has been replayed."""
+    if dev.type != "cuda" or torch.cuda.is_current_stream_capturing():
+        return torch.full((bs,), start, dtype=torch.int32, device=dev)
+    key = (bs, start, torch.cuda.current_stream(dev).cuda_stream)
+    hit = _POSITIONS.get(dev)
+    if hit is None or hit[0] != key:
+        hit = (key, torch.full((bs,), start, dtype=torch.int32, device=dev))
+        _POSITIONS[dev] = hit
+    return hit[1]
+
 
 class GroupedQueryAttention(nn.Module):
     def __init__(self, d_in: int, num_heads: int, n_kv_heads: int, head_dim: Optional[int] = None,
@@ -98,11 +117,11 @@ class GroupedQueryAttention(nn.Module):
             if seq_len == 1:
                 # one new token: QK-norm + RoPE + cache append fused into the
                 # split-KV decode kernel
-                seqlens = torch.full((bs,), total, dtype=torch.int32, device=dev)
+                seqlens = _positions(bs, total, dev)
                 kv_cache.cache_len = max(kv_cache.cache_len, total)
                 return self.decode_fused(qkv, cos, sin, kc_b, vc_b,
                                          seqlens).reshape(bs, seq_len, self.d_out)
-            positions = torch.full((bs,), start, dtype=torch.int32, device=dev)
+            positions = _positions(bs, start, dev)
             q = self.rope_cache(qkv, cos, sin, kc_b, vc_b, positions)
             kv_cache.cache_len = max(kv_cache.cache_len, start + seq_len)
             o = flash_attn_func(q, kc_b[:, :, :total].transpose(1, 2),
@@ -110,7 +129,7 @@ class GroupedQueryAttention(nn.Module):
         else:
             k = torch.empty(bs, self.n_kv_heads, seq_len, self.head_dim, dtype=qkv.dtype, device=dev)
             v = torch.empty_like(k)
-            positions = torch.zeros(bs, dtype=torch.int32, device=dev)
+            positions = _positions(bs, 0, dev)
             q = self.rope_cache(qkv, cos, sin, k, v, positions)
             o = flash_attn_func(q, k.transpose(1, 2), v.transpose(1, 2), causal=True)
         return o.reshape(bs, seq_len, self.d_out)
