@@ -32,7 +32,7 @@ int check_launch(const char *what) {
 // blockIdx % 8 running on one XCD. Once per device a probe launch records
 // HW_REG_XCC_ID for 512 workgroups; if any workgroup's XCD differs from that
 // of workgroup (id % 8), those kernels take their unfused paths on that
-// device. The probe needs a synchronous read back, so it is skipped (verdict
+// device. The probe needs a synchronous read back, so it is skipped (answer
 // "no", nothing cached) while the caller's stream is being captured, or when
 // the caller may not synchronise (may_probe false).
 constexpr int kXcdProbeBlocks = 512;
