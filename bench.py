@@ -293,9 +293,10 @@ def measure_configs():
         nxt = _rotating(lambda i: (randn(1, K, dtype=torch.float16),
                                    randn(Mo, K, dtype=torch.float16, std=0.02)), 96)
         cold, warm = _cold_warm(lambda x, W: C.gemv(x, W, None, 0), nxt, 96)
-        out.append(_cfg_entry(3, f"hgemv fp16 [1x{K}]x[{Mo}x{K}]^T", "hbm", cold, warm,
-                              (Mo * K + K + Mo) * 2))
+        hb = (Mo * K + K + Mo) * 2
         del nxt
+        out.append(_copy_ceiling(_cfg_entry(3, f"hgemv fp16 [1x{K}]x[{Mo}x{K}]^T", "hbm", cold, warm,
+                                            hb), hb, 96, randn))
     # decode attention B32 16/8 d128, cache 4096, bf16 ~N(0,1)
     B, L = 32, 4096
     kc = randn(B, Hkv, L, D, dtype=torch.bfloat16)
