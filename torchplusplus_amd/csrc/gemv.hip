@@ -322,7 +322,22 @@ __global__ __launch_bounds__(64 * MAXW) void gemv16_kernel(GemvArgs a, int64_t t
       __syncthreads();
     }
   } else if (x_res) {
-    load_x(k_begin, xa);
+    // Rows past the batch skip their input loads (a load under a branch, so
+    // the compiler waits for the first of them before the weight DMA goes
+    // out). Against the branch-free form (every lane loads, rows past the
+    // batch from the zero bytes), measured on three boxes: [1x3072] x
+    // [1024x3072]^T 4.08-4.13 against 4.35-4.40 us cold, o_proj at batch 8
+    // 4.40-4.65 against 4.66-4.72 us, the decode step equal to 1.4% shorter.
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int64_t c = k_begin + u * 32 + g * 8;
+      if (c < k_end && xok) {
+        xa[u] = *reinterpret_cast<const V8 *>(xr + c);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xa[u][i] = (T)0.0f;
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
     issue_w(blockIdx.x, ra);
   }
