@@ -201,15 +201,33 @@ def test_gemv_fused_input_rmsnorm(dev, bsz, n, k):
     close(y, oracle.linear_act(oracle.rmsnorm(x, nw, 1e-6), w), what="gemv(rmsnorm(x))")
 
 
-@pytest.mark.parametrize("n,k", [(1024, 2048), (1024, 3072), (1003, 1000)])
-def test_gemv_fused_residual_add(dev, n, k):
-    x, w, _ = _mk(8, n, k, torch.bfloat16, seed=11)
-    r = torch.randn(8, n, generator=torch.Generator().manual_seed(12)).bfloat16()
+@pytest.mark.parametrize("bsz", [1, 8, 16])
+@pytest.mark.parametrize("n,k", [(1024, 2048), (1024, 3072), (1003, 1000), (20000, 512), (1024, 5000)])
+def test_gemv_fused_residual_add(dev, bsz, n, k):
+    """Residual += x W^T: one tile per workgroup, workgroups looping over
+    several tiles (N = 20000: more tiles than workgroups, the next tile's
+    residual values requested with its weights), and K slices longer than
+    one load batch (K = 5000)."""
+    x, w, _ = _mk(bsz, n, k, torch.bfloat16, seed=11)
+    r = torch.randn(bsz, n, generator=torch.Generator().manual_seed(12)).bfloat16()
     rd = r.to(dev)
     out = ext().gemv_fused(x.to(dev), w.to(dev), None, 1e-6, rd)
     assert out.data_ptr() == rd.data_ptr()
     e = (r.float() + oracle.linear_act(x, w).float()).bfloat16()
     close(rd, e, what="residual += x W^T")
+
+
+@pytest.mark.parametrize("bsz", [3, 8])
+def test_gemv_fused_norm_and_residual(dev, bsz):
+    """Input RMSNorm and residual add in one GEMV (every wave loads the
+    residual values there, counted by the input's asm wait)."""
+    x, w, _ = _mk(bsz, 4096, 1024, torch.bfloat16, seed=13)
+    nw = (1 + 0.1 * torch.randn(1024, generator=torch.Generator().manual_seed(14))).bfloat16()
+    r = torch.randn(bsz, 4096, generator=torch.Generator().manual_seed(15)).bfloat16()
+    rd = r.to(dev)
+    ext().gemv_fused(x.to(dev), w.to(dev), nw.to(dev), 1e-6, rd)
+    e = (r.float() + oracle.linear_act(oracle.rmsnorm(x, nw, 1e-6), w).float()).bfloat16()
+    close(rd, e, what="residual += rmsnorm(x) W^T")
 
 
 def test_gemv_swiglu_with_input_norm(dev):
