@@ -251,13 +251,19 @@ __global__ __launch_bounds__(256) void ffn_decode_kernel(FfnArgs a) {
   // h stores reached this XCD's L2 (vmcnt(0), which also covers the down
   // DMA); one thread counts the workgroup in and waits for the XCD's other
   // 31. The counter is reset after phase 2 by the XCD's last workgroup to
-  // leave (depart below), off this critical path.
+  // leave (depart below), off this critical path. The poll is an atomic add
+  // of 0, performed in the XCD's L2 where the arrivals are counted; an
+  // agent-scope load goes past the L2 on every poll (measured: decode step
+  // 1.115 -> 1.082 ms with the atomic). The 0 comes from an asm move: the
+  // compiler turns an atomic add of a known 0 back into that load.
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
   if (threadIdx.x == 0) {
     __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     unsigned n = 0;
-    while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < kFfnPerXcd) {
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    while (__hip_atomic_fetch_add(arrive, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < kFfnPerXcd) {
       if (++n > kFfnSpinLimit) {
         __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
