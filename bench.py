@@ -167,10 +167,11 @@ def measure_kernels(model, dec, cfg, L):
     out.append(mfma_entry("gemm swiglu [16384x1024]x[6144x1024]^T", t, 2 * M * 2 * I * E))
     qp = torch.randn(BATCH, PREFILL, H, D, generator=g, device=dev).to(dt)
     kp = torch.randn(BATCH, PREFILL, Hkv, D, generator=g, device=dev).to(dt)
-    t = event_time_us(lambda: C.flash_attn_func(qp, kp, kp, True, -1, -1, 0.0), 4)
+    vp = torch.randn(BATCH, PREFILL, Hkv, D, generator=g, device=dev).to(dt)
+    t = event_time_us(lambda: C.flash_attn_func(qp, kp, vp, True, -1, -1, 0.0), 4)
     keys = PREFILL * (PREFILL + 1) // 2
     out.append(mfma_entry("attn_prefill causal B8 S2048 16/8 d128", t, 4 * BATCH * H * D * keys))
-    del xp, qp, kp
+    del xp, qp, kp, vp
     return out, attn_us, attn_bytes
 
 
@@ -313,8 +314,8 @@ def measure_configs():
 
 def cpu_configs(configs):
     """The oracle (PyTorch CPU restatement of each reference op) timed on the
-    host cores beside every BASELINE config entry: median of 3 calls after one
-    warm-up, same shapes and dtypes (attention on a 1-sequence sample, scaled
+    host cores beside every BASELINE config entry: median of 5 calls after two
+    warm-ups, same shapes and dtypes (attention on a 1-sequence sample, scaled
     to the config's batch; noted in `cpu_sample`)."""
     import oracle
 
@@ -324,7 +325,8 @@ def cpu_configs(configs):
     def rnd(*shape, dtype, std=1.0, mean=0.0):
         return (mean + std * torch.randn(*shape, generator=g)).to(dtype)
 
-    def med_us(fn, reps=3):
+    def med_us(fn, reps=5):
+        fn()
         fn()
         ts = []
         for _ in range(reps):
@@ -371,26 +373,81 @@ def cpu_configs(configs):
                 break
 
 
-def cpu_baseline(model, cfg, steps: int = 3):
+def cpu_model_name() -> str:
+    """The host CPU's model name (/proc/cpuinfo, as lscpu reports it)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median(ts):
+    ts = sorted(ts)
+    return ts[len(ts) // 2]
+
+
+def cpu_baseline(model, cfg, steps: int = 5, warmup: int = 2, full: bool = False, reps: int = 5):
     """The oracle's eager PyTorch decode (fp32 math, bf16 rounding at op
-    boundaries) on this host: batch 8, synthetic 2048-position cache."""
+    boundaries) on this host's cores, batch 8.
+
+    Default (bounded sample, ~10-30 s of CPU work so the bench stays within
+    minutes): `warmup` decode steps, then `steps` timed decode steps against a
+    2048-position cache filled with random K/V (a decode step costs the same
+    whatever the cache holds); value = batch / median step time.
+    full=True: the complete CPU plan -- per rep a 2048-token batch-8 prefill
+    followed by 32 greedy decode steps, `warmup` + `reps` reps, medians of
+    the per-rep prefill time and decode step time (several minutes per rep)."""
     from oracle.qwen3 import Qwen3Oracle
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    orc = Qwen3Oracle(model.state_dict(), cfg, PREFILL + steps + 2)
     g = torch.Generator().manual_seed(2)
-    orc.seed_cache(BATCH, PREFILL, g)
-    ids = torch.randint(0, cfg.vocab_size, (BATCH, 1), generator=g)
-    orc.forward(ids, PREFILL)  # warm-up step
-    t0 = time.perf_counter()
-    for s in range(steps):
-        logits = orc.forward(ids, PREFILL + 1 + s)
-        ids = logits[:, -1].argmax(-1, keepdim=True)
-    dt = time.perf_counter() - t0
-    return {"value": round(BATCH * steps / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{steps} greedy decode steps, batch {BATCH}, cache {PREFILL} positions "
-                      f"(random K/V), after 1 warm-up step; oracle/qwen3.py on the host CPU"}
+    base = {"unit": "tok/s", "cores": cores, "kind": "port", "cpu_model": cpu_model_name(),
+            "timer": "time.perf_counter"}
+    if not full:
+        orc = Qwen3Oracle(model.state_dict(), cfg, PREFILL + warmup + steps + 2)
+        orc.seed_cache(BATCH, PREFILL, g)
+        ids = torch.randint(0, cfg.vocab_size, (BATCH, 1), generator=g)
+        ts = []
+        for s in range(warmup + steps):
+            t0 = time.perf_counter()
+            logits = orc.forward(ids, PREFILL + s)
+            ids = logits[:, -1].argmax(-1, keepdim=True)
+            if s >= warmup:
+                ts.append(time.perf_counter() - t0)
+        step = _median(ts)
+        return {**base, "value": round(BATCH / step, 3), "ms_per_step": round(step * 1e3, 1),
+                "sample": f"bounded sample: {warmup} warm-up + {steps} timed greedy decode steps "
+                          f"(median), batch {BATCH}, cache {PREFILL} positions of random K/V; "
+                          f"oracle/qwen3.py on the host CPU. The full plan (2048-token prefill + "
+                          f"32 steps, median of 5) runs with --cpu-full"}
+    n_dec = 32
+    pre, dec = [], []
+    for r in range(warmup + reps):
+        orc = Qwen3Oracle(model.state_dict(), cfg, PREFILL + n_dec + 2)
+        ids = torch.randint(0, cfg.vocab_size, (BATCH, PREFILL), generator=g)
+        t0 = time.perf_counter()
+        logits = orc.forward(ids, 0)
+        t1 = time.perf_counter()
+        nxt = logits[:, -1].argmax(-1, keepdim=True)
+        for s in range(n_dec):
+            logits = orc.forward(nxt, PREFILL + s)
+            nxt = logits[:, -1].argmax(-1, keepdim=True)
+        t2 = time.perf_counter()
+        log(f"[bench] cpu full rep {r}: prefill {t1 - t0:.1f} s, {n_dec} steps {t2 - t1:.1f} s")
+        if r >= warmup:
+            pre.append(t1 - t0)
+            dec.append((t2 - t1) / n_dec)
+    step = _median(dec)
+    return {**base, "value": round(BATCH / step, 3), "ms_per_step": round(step * 1e3, 1),
+            "prefill_s": round(_median(pre), 2),
+            "prefill_tok_per_s": round(BATCH * PREFILL / _median(pre), 1),
+            "sample": f"full plan: {warmup} warm-up + {reps} reps (medians) of a {PREFILL}-token "
+                      f"batch-{BATCH} prefill then {n_dec} greedy decode steps; oracle/qwen3.py"}
 
 
 TRAFFIC_GROUPS = ["attn", "gemv_qkv", "gemv_o", "gemv_gu", "gemv_down", "ffn", "lm_head", "rmsnorm",
@@ -540,7 +597,11 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=8)
+    ap.add_argument("--cpu-steps", type=int, default=5)
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="CPU baseline as full 2048-token prefill + 32 decode steps, 2 warm-ups, "
+                         "median of 5 reps (several minutes per rep)")
+    ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--traffic-probe", nargs="?", const="attn", choices=TRAFFIC_GROUPS,
                     help="only launch one HBM-bound kernel group + a calibration copy (for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE); attn at cache length "
@@ -617,7 +678,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
-        cpu = cpu_baseline(model, cfg, args.cpu_steps)
+        cpu = cpu_baseline(model, cfg, args.cpu_steps, full=args.cpu_full, reps=args.cpu_reps)
         cpu_configs(configs)
         log("[bench] cpu config timings done")
 

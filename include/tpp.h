@@ -53,6 +53,19 @@ const char *tpp_last_error_string(void);
 /* ABI version, (major << 16) | minor. */
 int tpp_version(void);
 
+/* One-time checks of the current device for the kernels that synchronise
+ * workgroups inside one XCD (the decode attention's in-kernel split merge,
+ * the one-launch decode FFN): the CU count and a probe launch that records
+ * each workgroup's XCD. Runs the probe on `stream` and synchronises it; fails
+ * with TPP_E_INVALID while `stream` is being captured. Those kernels run the
+ * same checks on their first call; a first call made during a capture cannot
+ * probe and takes the unfused path (two launches, correct), so call this
+ * before capturing a graph. *xcd_local (optional) = 1 if workgroups with
+ * equal blockIdx % 8 share an XCD, *cu_count (optional) = the CU count (the
+ * one-launch FFN needs 256). No counterpart in the reference, whose kernels
+ * never exchange data inside a launch. */
+int tpp_prepare_device(void *stream, int *xcd_local, int *cu_count);
+
 /* ---- normalisation ------------------------------------------------------- */
 
 /* y[m,:] = x[m,:] * rsqrt(mean(x[m,:]^2) + eps) * w, fp32 math, one rounding.
@@ -192,10 +205,17 @@ int tpp_ffn_decode(void *residual, const void *norm_w, float eps,
                    int64_t I, int dtype, void *workspace, size_t ws_bytes,
                    void *stream);
 
-/* Test hook: *out = nonzero if a tpp_ffn_decode launch on this workspace
- * ever gave up waiting for its workgroups (never expected; the output of
- * such a launch is wrong). Synchronises `stream`. */
-int tpp_ffn_decode_sync_errors(const void *workspace, int *out, void *stream);
+/* *out = nonzero if a one-launch tpp_ffn_decode on this workspace gave up
+ * waiting for its workgroups since the last call. That launch needs all 256
+ * workgroups resident at once; if they are not (other work holding CUs),
+ * its bounded wait ends, a flag in the workspace is set, and its output is
+ * WRONG. When the flag is set this call also zeroes the workspace's counter
+ * region and the flag, so later launches are correct again. Call it where
+ * the caller synchronises anyway (after a decode loop) with no tpp_ffn_decode
+ * on this workspace in flight; it synchronises `stream` and fails during
+ * stream capture. No counterpart in the reference, whose kernels never wait
+ * on one another. */
+int tpp_ffn_decode_sync_errors(void *workspace, int *out, void *stream);
 
 /* Workspace bytes of tpp_gemv_argmax (no initialisation required). */
 size_t tpp_gemv_argmax_workspace_size(int64_t B, int64_t N);

@@ -211,21 +211,72 @@ def test_decode_fused_prologue_matches_unfused(dev, hq, hkv, norm):
     got = C.attn_decode_fused(qkv, qw, kw, cos, sin, 1e-6, kc, vc, pos + 1)
     assert torch.equal(kc, kc2) and torch.equal(vc, vc2), "cache append differs"
     close(got, ref, atol=1e-2, rtol=1e-2, what="fused decode")
-    # independent of the HIP prologue: q and the appended K/V from the oracle
-    # (QK-RMSNorm over D, RoPE at position pos[b], torchpp/attention/gqa.py:90-116)
-    x = qkv.cpu().view(B, hq + 2 * hkv, D)
+    e, k_ref, v_ref = _fused_decode_oracle(qkv.cpu(), hq, hkv, qw, kw, cos.cpu(), sin.cpu(),
+                                           kc2.cpu(), vc2.cpu(), pos.cpu())
+    close(kc.cpu(), k_ref, what="fused decode: appended K vs oracle")
+    assert torch.equal(vc.cpu(), v_ref), "fused decode: appended V differs from the projection"
+    close(got, e, what="fused decode vs oracle")
+
+
+def _fused_decode_oracle(qkv, hq, hkv, qw, kw, cos, sin, k_before, v_before, pos):
+    """Independent of the HIP prologue: q and the appended K/V from the oracle
+    (QK-RMSNorm over D, RoPE at position pos[b], V as projected;
+    torchpp/attention/gqa.py:90-116, kvcache.py:50-108), then decode attention
+    over pos[b] + 1 keys. Returns (output, K cache, V cache) on the CPU."""
+    B, D = k_before.shape[0], k_before.shape[-1]
+    x = qkv.view(B, hq + 2 * hkv, D)
     qh, kh, vh = x[:, :hq], x[:, hq:hq + hkv], x[:, hq + hkv:]
-    if norm:
+    if qw is not None:
         qh, kh = oracle.rmsnorm(qh, qw.cpu(), 1e-6), oracle.rmsnorm(kh, kw.cpu(), 1e-6)
-    pl = pos.cpu().long()
-    cr, sr = cos.cpu()[pl][:, None], sin.cpu()[pl][:, None]  # [B, 1, D]
+    pl = pos.long()
+    cr, sr = cos[pl][:, None], sin[pl][:, None]  # [B, 1, D]
     qh, kh = oracle.rope(qh[:, :, None], cr[:, :, None], sr[:, :, None])[:, :, 0], \
         oracle.rope(kh[:, :, None], cr[:, :, None], sr[:, :, None])[:, :, 0]
-    k_ref, v_ref = kc2.cpu().clone(), vc2.cpu().clone()
+    k_ref, v_ref = k_before.clone(), v_before.clone()
     for b in range(B):
         k_ref[b, :, pl[b]] = kh[b]
         v_ref[b, :, pl[b]] = vh[b]
-    close(kc.cpu(), k_ref, what="fused decode: appended K vs oracle")
-    assert torch.equal(vc.cpu(), v_ref), "fused decode: appended V differs from the projection"
-    e = oracle.decode_attention(qh[:, None], k_ref, v_ref, (pos + 1).tolist())
-    close(got, e, what="fused decode vs oracle")
+    return oracle.decode_attention(qh[:, None], k_ref, v_ref, (pl + 1).tolist()), k_ref, v_ref
+
+
+@pytest.mark.parametrize("lens", [[2049] * 8, [2068] * 8, [2068, 2049, 2060, 1921, 1920, 641, 640, 1]],
+                         ids=["L2049", "L2068", "ragged"])
+def test_decode_fused_model_shape_split_merge(dev, lens):
+    """The roofline kernel at its own shape: the decode step of the benchmark
+    (batch 8, 16/8 heads, D 128, a 2069-row cache, cache lengths 2049..2068
+    over the driver's 20 steps), where each (batch, KV head) pair's keys are
+    split over 4 workgroups of 640 keys (the last split 129-148 keys) merged
+    in-kernel by the pair's last workgroup. All 8 sequences and the K/V append
+    against the oracle; the ragged case has splits with no key at all."""
+    import ctypes
+
+    import torchplusplus_amd
+    from torchplusplus_amd._native import ext, lib
+
+    C = ext()
+    B, hq, hkv, D, Lmax = 8, 16, 8, 128, 2069
+    f = lib().tpp_attn_decode_workspace_size
+    f.restype = ctypes.c_size_t
+    ws = f(*(ctypes.c_int64(v) for v in (B, hq, hkv, D, Lmax)))
+    assert ws == 64 * 1024 + B * hq * 4 * (D + 32) * 4, f"plan is not 4 splits ({ws} B)"
+    info = torchplusplus_amd.prepare_device(dev)
+    assert info["xcd_local"], "XCD placement probe failed: the split merge would run unfused"
+    g = torch.Generator().manual_seed(21)
+    qkv = torch.randn(B, 1, (hq + 2 * hkv) * D, generator=g).bfloat16()
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    cos, sin = oracle.compute_rope_params(D, 1e6, Lmax + 1)
+    kc = torch.randn(B, hkv, Lmax, D, generator=g).bfloat16()
+    vc = torch.randn(B, hkv, Lmax, D, generator=g).bfloat16()
+    seqlens = torch.tensor(lens, dtype=torch.int32)
+    e, k_ref, v_ref = _fused_decode_oracle(qkv, hq, hkv, qw, kw, cos, sin, kc, vc, seqlens - 1)
+    kd, vd = kc.to(dev), vc.to(dev)
+    got = C.attn_decode_fused(qkv.to(dev), qw.to(dev), kw.to(dev), cos.to(dev), sin.to(dev), 1e-6,
+                              kd, vd, seqlens.to(dev))
+    close(kd.cpu(), k_ref, what="model-shape fused decode: appended K")
+    assert torch.equal(vd.cpu(), v_ref), "model-shape fused decode: appended V"
+    close(got, e, what="model-shape fused decode vs oracle")
+    # a second call over the same workspace (its arrival counters back at zero)
+    got2 = C.attn_decode_fused(qkv.to(dev), qw.to(dev), kw.to(dev), cos.to(dev), sin.to(dev), 1e-6,
+                               kd, vd, seqlens.to(dev))
+    assert torch.equal(got, got2), "repeated call differs"

@@ -5,7 +5,7 @@ import torch
 
 from oracle.qwen3 import Qwen3Oracle
 from tests.conftest import close
-from torchplusplus_amd.fastqwen3 import FastQwen3, GreedyDecoder, QwenConfig
+from torchplusplus_amd.fastqwen3 import FastQwen3, GreedyDecoder, QwenConfig, QwenConfig_float16
 
 pytestmark = pytest.mark.gpu
 
@@ -25,6 +25,9 @@ def model_close(got, exp, what):
 
 TINY = QwenConfig(vocab_size=1000, context_length=512, embed_dim=256, n_heads=4, n_layers=2,
                   head_dim=128, n_kv_heads=2, hidden_dim=512, dtype=torch.bfloat16)
+# the reference's own model config is fp16 (QwenConfig_float16, fastqwen3.py:15-27)
+TINY16 = QwenConfig_float16(vocab_size=1000, context_length=512, embed_dim=256, n_heads=4,
+                            n_layers=2, head_dim=128, n_kv_heads=2, hidden_dim=512)
 
 
 def _model(dev, cfg=TINY, seed=0):
@@ -39,12 +42,13 @@ def _model(dev, cfg=TINY, seed=0):
     return m
 
 
+@pytest.mark.parametrize("cfg", [TINY, TINY16], ids=["bf16", "fp16"])
 @torch.inference_mode()
-def test_prefill_and_teacher_forced_decode(dev):
-    m = _model(dev)
-    orc = Qwen3Oracle(m.state_dict(), TINY, TINY.context_length)
+def test_prefill_and_teacher_forced_decode(dev, cfg):
+    m = _model(dev, cfg)
+    orc = Qwen3Oracle(m.state_dict(), cfg, cfg.context_length)
     B, S = 3, 40
-    ids = torch.randint(0, TINY.vocab_size, (B, S + 4), generator=torch.Generator().manual_seed(1))
+    ids = torch.randint(0, cfg.vocab_size, (B, S + 4), generator=torch.Generator().manual_seed(1))
     m.setup_kv_cache(64, B)
     m.reset_kv_cache()
     got = m.forward(ids[:, :S].to(dev), use_cache=True, cache_position=0)
@@ -67,11 +71,12 @@ def test_forward_without_cache_matches_cached_prefill(dev):
     close(a, b, atol=1e-2, rtol=1e-2, what="no-cache vs cache prefill")
 
 
+@pytest.mark.parametrize("cfg", [TINY, TINY16], ids=["bf16", "fp16"])
 @torch.inference_mode()
-def test_graph_decode_equals_eager_decode(dev):
-    m = _model(dev, seed=4)
+def test_graph_decode_equals_eager_decode(dev, cfg):
+    m = _model(dev, cfg, seed=4)
     B, S, N = 4, 17, 12
-    ids = torch.randint(0, TINY.vocab_size, (B, S), generator=torch.Generator().manual_seed(5)).to(dev)
+    ids = torch.randint(0, cfg.vocab_size, (B, S), generator=torch.Generator().manual_seed(5)).to(dev)
     eager = m.generate_greedy(ids, N, use_graph=False)
     graph = m.generate_greedy(ids, N, use_graph=True)
     assert torch.equal(eager, graph)

@@ -24,7 +24,7 @@ import torch
 from oracle.qwen3 import Qwen3Oracle
 from tests.conftest import close
 from tests.test_model import MODEL_ATOL, MODEL_RTOL
-from torchplusplus_amd.fastqwen3 import FastQwen3, QwenConfig
+from torchplusplus_amd.fastqwen3 import FastQwen3, QwenConfig, QwenConfig_float16
 
 pytestmark = pytest.mark.gpu
 
@@ -39,10 +39,9 @@ def model(dev):
     return m
 
 
-@torch.inference_mode()
-def test_config5_prefill_and_greedy_decode(dev, model):
+def _prefill_and_greedy_decode(dev, model, cfg):
     B, S, N = 8, 2048, 9
-    ids = torch.randint(0, CFG.vocab_size, (B, S), generator=torch.Generator().manual_seed(1)).to(dev)
+    ids = torch.randint(0, cfg.vocab_size, (B, S), generator=torch.Generator().manual_seed(1)).to(dev)
     graph = model.generate_greedy(ids, N, use_graph=True)
     eager = model.generate_greedy(ids, N, use_graph=False)
     assert graph.shape == (B, S + N)
@@ -52,6 +51,23 @@ def test_config5_prefill_and_greedy_decode(dev, model):
     logits = model.forward_impl(ids, model.kv_cache_array, 0, last_only=True)
     assert torch.isfinite(logits.float()).all()
     assert torch.equal(graph[:, S], logits[:, -1].float().argmax(-1))
+
+
+@torch.inference_mode()
+def test_config5_prefill_and_greedy_decode(dev, model):
+    _prefill_and_greedy_decode(dev, model, CFG)
+
+
+@torch.inference_mode()
+def test_config5_fp16_prefill_and_greedy_decode(dev):
+    """The same at the reference's own dtype (QwenConfig_float16,
+    examples/LLM/fastqwen3.py:15-27)."""
+    cfg = QwenConfig_float16()
+    m = FastQwen3(cfg, device=dev, rope_context=ROPE_CTX).eval()
+    m.init_weights(std=0.02, generator=torch.Generator(device=dev).manual_seed(0))
+    _prefill_and_greedy_decode(dev, m, cfg)
+    del m
+    torch.cuda.empty_cache()
 
 
 def _rel(a, b):

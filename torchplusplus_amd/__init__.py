@@ -46,3 +46,19 @@ def _install_compat() -> None:
 
 
 _install_compat()
+
+
+def prepare_device(device=None) -> dict:
+    """One-time checks of a GPU for the kernels that exchange data inside one
+    XCD (the decode attention's in-kernel split merge, the one-launch decode
+    FFN): a workgroup placement probe and the CU count. Synchronises the
+    device's current stream; call it before capturing a HIP graph (a first
+    call of those kernels inside a capture cannot probe and takes their
+    two-launch paths). Returns {"xcd_local": bool, "cu_count": int}."""
+    import torch
+
+    from torchplusplus_amd._native import ext
+
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    xcd, cus = ext().prepare_device(torch.empty(0, device=dev))
+    return {"xcd_local": bool(xcd), "cu_count": int(cus)}

@@ -7,8 +7,9 @@ Same constructor and forward signature. Per call the layer runs:
   3. flash attention with native GQA (no repeat_interleave / .contiguous()
      copies), or split-KV decode attention when a single token is appended
   4. the output projection.
-The fused projection weight is built from Wq/Wk/Wv on first use; call
-`refresh_fused_weights()` after changing those parameters.
+The fused projection weight is built from Wq/Wk/Wv on first use and rebuilt
+whenever one of them changes (load_state_dict, in-place edits), as the
+reference reads its projection weights on every call (gqa.py:82-84).
 """
 from __future__ import annotations
 
@@ -19,6 +20,7 @@ import torch.nn as nn
 
 from torchplusplus_amd._native import ext as _ext
 from torchplusplus_amd.attention.flash import flash_attn_func
+from torchplusplus_amd.dlops.derived import DerivedWeight, attach
 from torchplusplus_amd.dlops.linear import linear
 from torchplusplus_amd.llmops.kvcache import KVCache
 
@@ -69,16 +71,16 @@ class GroupedQueryAttention(nn.Module):
         else:
             self.q_norm = self.k_norm = None
         self.DEBUG = DEBUG
-        self._wqkv = None
+        self._wqkv = attach(self, DerivedWeight(lambda q, k, v: torch.cat([q, k, v], 0).contiguous()))
 
     def refresh_fused_weights(self):
-        with torch.no_grad():
-            self._wqkv = torch.cat([self.Wq.weight, self.Wk.weight, self.Wv.weight], 0).contiguous()
+        """Force a rebuild of the fused projection weight."""
+        self._wqkv.invalidate()
+        self.fused_qkv_weight()
 
     def fused_qkv_weight(self) -> torch.Tensor:
-        if self._wqkv is None or self._wqkv.device != self.Wq.weight.device:
-            self.refresh_fused_weights()
-        return self._wqkv
+        """[(Hq+2Hkv)*D, d_in]: Wq, Wk, Wv stacked, current with the parameters."""
+        return self._wqkv.get(self.Wq.weight, self.Wk.weight, self.Wv.weight)
 
     def rope_cache(self, qkv, cos, sin, k_dst, v_dst, positions):
         """Step 2 on a projected qkv [B, S, (Hq+2Hkv)*D]: returns q [B, S, Hq, D];

@@ -1018,11 +1018,13 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
   __syncthreads();
   const int pair = b * p.Hkv + hk;
   if (threadIdx.x == 0) {
+    // agent scope: the counter is shared by workgroups (of one XCD); the
+    // atomic is performed in that XCD's L2 either way
     const int old = __hip_atomic_fetch_add(&counters[pair], 1, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+                                           __HIP_MEMORY_SCOPE_AGENT);
     s_last = old == nsplit - 1;
     if (old == nsplit - 1) // leave the counter at 0 for the next launch
-      __hip_atomic_store(&counters[pair], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_store(&counters[pair], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!s_last) return;

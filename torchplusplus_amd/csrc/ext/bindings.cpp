@@ -438,13 +438,16 @@ std::vector<at::Tensor> gemv_argmax(at::Tensor input, at::Tensor weight,
 // calls, and the old one is kept alive (`retired`) until the process ends:
 // a graph captured earlier still holds its address in its kernel arguments
 // and keeps using it (its counters stay zero, since only that graph's calls
-// touch it). Slot 1 belongs to decode attention alone: its arrival counters
-// must stay zero between calls, which the kernel guarantees but another user
-// of the same bytes would not. Calls that share a slot must not overlap, so a
-// call on a stream other than the slot's last one first makes its stream
-// wait for that stream (an event); while a stream is being captured the
-// capture is ordered after earlier work by the caller (torch.cuda.graph
-// synchronizes first).
+// touch it). Slots 1 (decode attention) and 2 (decode FFN) hold counters
+// that must be zero before a call and that every call leaves at zero, which
+// the kernels guarantee but another user of the same bytes would not; such a
+// slot is therefore created or grown only outside stream capture (a zero
+// fill recorded into a graph would leave the buffer unset for eager calls
+// until the graph ran): the call is refused with a message instead. Calls
+// that share a slot must not overlap, so a call on a stream other than the
+// slot's last one first makes its stream wait for that stream (an event);
+// while a stream is being captured the capture is ordered after earlier
+// work by the caller (torch.cuda.graph synchronizes first).
 struct ScratchSlot {
   at::Tensor t;
   std::vector<at::Tensor> retired;
@@ -452,12 +455,16 @@ struct ScratchSlot {
   hipEvent_t ev = nullptr;
 };
 
-at::Tensor cached_workspace(const at::Tensor &like, size_t bytes, int slot = 0) {
-  constexpr int kSlots = 3; // 0: greedy-step argmax partials, 1: decode attention, 2: decode FFN
+constexpr int kSlots = 3; // 0: greedy-step argmax partials, 1: decode attention, 2: decode FFN
+
+ScratchSlot &scratch_slot(int dev, int slot) {
   static std::vector<ScratchSlot> *cache = new std::vector<ScratchSlot>(64 * kSlots);
-  const int dev = like.device().index();
   TORCH_CHECK(dev >= 0 && dev < 64 && slot >= 0 && slot < kSlots, "device index out of range");
-  ScratchSlot &e = (*cache)[dev * kSlots + slot];
+  return (*cache)[dev * kSlots + slot];
+}
+
+at::Tensor cached_workspace(const at::Tensor &like, size_t bytes, int slot = 0) {
+  ScratchSlot &e = scratch_slot(like.device().index(), slot);
   hipStream_t s = (hipStream_t)cur_stream(like);
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   TORCH_CHECK(hipStreamIsCapturing(s, &cs) == hipSuccess, "hipStreamIsCapturing failed");
@@ -468,6 +475,10 @@ at::Tensor cached_workspace(const at::Tensor &like, size_t bytes, int slot = 0) 
                 "ordering the shared workspace between streams failed");
   }
   if (!e.t.defined() || (size_t)e.t.numel() * 4 < bytes) {
+    TORCH_CHECK(!capturing || slot == 0,
+                slot == 1 ? "attn_decode" : "ffn_decode",
+                ": its device workspace is created (or grown) on the first call of a shape, which "
+                "cannot be inside stream capture; run the call once before capturing");
     int64_t n = (int64_t)((bytes + 3) / 4);
     n = n < (1 << 20) ? (1 << 20) : n;
     if (e.t.defined()) e.retired.push_back(e.t);
@@ -503,15 +514,38 @@ void ffn_decode(at::Tensor residual, at::Tensor norm_w, double eps, at::Tensor w
            "ffn_decode");
 }
 
-// nonzero if a fused decode FFN launch on this device's workspace ever gave
-// up waiting for its workgroups (test hook; synchronises the stream)
+// nonzero if a one-launch decode FFN on this device gave up waiting for its
+// workgroups (its output was wrong) since the last check; reads and clears
+// the flag of every workspace the device's FFN calls may use (the current
+// one and the retired ones that captured graphs still hold). Synchronises
+// the current stream after ordering it behind the workspace's last stream.
 int64_t ffn_decode_sync_errors(at::Tensor like) {
+  TORCH_CHECK(like.is_cuda(), "ffn_decode_sync_errors: expected a CUDA tensor");
   c10::DeviceGuard g(like.device());
-  at::Tensor ws = cached_workspace(like, 1, 2);
-  int out = 0;
-  check_rc(tpp_ffn_decode_sync_errors(ws.data_ptr(), &out, cur_stream(like)),
-           "ffn_decode_sync_errors");
-  return out;
+  ScratchSlot &e = scratch_slot(like.device().index(), 2);
+  if (!e.t.defined()) return 0; // no FFN call on this device yet
+  cached_workspace(like, 1, 2); // orders this stream after the slot's last one
+  int64_t any = 0;
+  auto check = [&](at::Tensor &t) {
+    int out = 0;
+    check_rc(tpp_ffn_decode_sync_errors(t.data_ptr(), &out, cur_stream(like)),
+             "ffn_decode_sync_errors");
+    any |= out;
+  };
+  check(e.t);
+  for (auto &t : e.retired) check(t);
+  return any;
+}
+
+// One-time device checks of the XCD-local kernels, outside capture
+// (tpp_prepare_device): returns (workgroups with equal id % 8 share an XCD,
+// CU count).
+std::tuple<bool, int64_t> prepare_device(at::Tensor like) {
+  TORCH_CHECK(like.is_cuda(), "prepare_device: expected a CUDA tensor");
+  c10::DeviceGuard g(like.device());
+  int xcd = 0, cus = 0;
+  check_rc(tpp_prepare_device(cur_stream(like), &xcd, &cus), "prepare_device");
+  return {xcd != 0, (int64_t)cus};
 }
 
 // greedy decode tail: ids <- argmax(lm_head(norm(input))), resid_next <-
@@ -701,7 +735,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("residual"), py::arg("norm_weight"), py::arg("eps"), py::arg("w_gu"),
         py::arg("w_down"));
   m.def("ffn_decode_sync_errors", &ffn_decode_sync_errors,
-        "test hook: nonzero if a fused decode FFN launch gave up waiting for its workgroups",
+        "nonzero if a one-launch decode FFN gave up waiting for its workgroups since the last "
+        "check (its output was wrong); clears the flag",
+        py::arg("like"));
+  m.def("prepare_device", &prepare_device,
+        "one-time XCD placement probe and CU count of the tensor's device (outside capture)",
         py::arg("like"));
   m.def("argmax_rows", &argmax_rows, "argmax over the last dim (greedy sampling)", py::arg("x"));
   m.def("flash_attn_func", &attn_fwd, "flash attention forward (GQA, causal, window)",

@@ -422,11 +422,30 @@ extern "C" int tpp_ffn_decode(void *residual, const void *norm_w, float eps, con
   });
 }
 
-extern "C" int tpp_ffn_decode_sync_errors(const void *workspace, int *out, void *stream) {
-  if (!workspace || !out) return set_error(TPP_E_INVALID, "tpp_ffn_decode_sync_errors: null pointer");
-  if (hipMemcpyAsync(out, (const char *)workspace + kFfnOffErr, sizeof(int), hipMemcpyDeviceToHost,
-                     as_stream(stream)) != hipSuccess ||
-      hipStreamSynchronize(as_stream(stream)) != hipSuccess)
-    return set_error(TPP_E_LAUNCH, "tpp_ffn_decode_sync_errors: copy failed");
+extern "C" int tpp_ffn_decode_sync_errors(void *workspace, int *out, void *stream) {
+  const char *name = "tpp_ffn_decode_sync_errors";
+  if (!workspace || !out) return set_error(TPP_E_INVALID, "%s: null pointer", name);
+  hipStream_t st = as_stream(stream);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return set_error(TPP_E_INVALID, "%s: not callable while the stream is being captured", name);
+  }
+  int flag = 0;
+  if (hipMemcpyAsync(&flag, (const char *)workspace + kFfnOffErr, sizeof(int),
+                     hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(TPP_E_LAUNCH, "%s: copy failed", name);
+  }
+  // a launch that gave up leaves its counters in an unknown state (late
+  // workgroups count in after the reset): zero them and the flag, so the
+  // workspace is usable again
+  if (flag && (hipMemsetAsync(workspace, 0, kFfnCtrBytes, st) != hipSuccess ||
+               hipStreamSynchronize(st) != hipSuccess)) {
+    (void)hipGetLastError();
+    return set_error(TPP_E_LAUNCH, "%s: clearing the counters failed", name);
+  }
+  *out = flag;
   return TPP_OK;
 }

@@ -379,10 +379,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
           if (m % SP == 0 && m / SP <= NQ && more) issue_one(kn % NST, kn, m / SP - 1);
           if (m == MID && next) {
             // own DMA of K tile kt + 1 landed (tiles kt + 2 .. kt + NST - 1
-            // may still be in flight); the fragment reads of tile kt all
-            // returned (the MFMAs above consumed them), so after the barrier
-            // its slot may be refilled by any wave
+            // may still be in flight). The fragment reads of tile kt must
+            // all have returned before the barrier, since after it any wave
+            // may refill that slot: with one row block per wave (FM = 1) the
+            // fragments of the second half of this sub-step are not consumed
+            // yet, so wait for every LDS read (lgkmcnt(0); the barrier does
+            // not wait for them)
             wait_tiles<NQ, NST - 2>(nk - kt - 2);
+            wait_lgkmcnt0();
             __builtin_amdgcn_s_barrier();
             frag(smem + ((kt + 1) % NST) * STG, 0);
           }
@@ -610,11 +614,13 @@ __global__ __launch_bounds__(512) void gemm_persist_kernel(
             if (m % SP == 0 && m / SP <= NQ && dma) issue(ds, slot ^ 1, kd, m / SP - 1);
             if (m == MID && more) {
               // the other slot's DMA landed; this slot's fragment reads all
-              // returned (the MFMAs above consumed them). Vector memory
-              // operations complete in issue order, so behind an early DMA
-              // only the epilogue stores issued after it may stay in flight.
+              // returned (lgkmcnt(0): the slot is refilled after the
+              // barrier). Vector memory operations complete in issue order,
+              // so behind an early DMA only the epilogue stores issued after
+              // it may stay in flight.
               if (early && sto == NSTO) wait_vmcnt<NSTO>();
               else wait_vmcnt<0>();
+              wait_lgkmcnt0();
               __builtin_amdgcn_s_barrier();
               frag(smem + (slot ^ 1) * STG, 0);
             }

@@ -100,5 +100,26 @@ int device_cu_count() {
 
 } // namespace tpp
 
+extern "C" int tpp_prepare_device(void *stream, int *xcd_local, int *cu_count) {
+  using namespace tpp;
+  const char *name = "tpp_prepare_device";
+  hipStream_t st = (hipStream_t)stream;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(TPP_E_INVALID, "%s: hipStreamIsCapturing failed", name);
+  }
+  if (cs != hipStreamCaptureStatusNone)
+    return set_error(TPP_E_INVALID, "%s: the stream is being captured; call it before the capture",
+                     name);
+  const int cus = device_cu_count();
+  if (cus <= 0) return set_error(TPP_E_LAUNCH, "%s: no current HIP device", name);
+  const bool ok = xcd_grouping_holds(st, true);
+  if (xcd_local) *xcd_local = ok ? 1 : 0;
+  if (cu_count) *cu_count = cus;
+  g_err[0] = 0;
+  return TPP_OK;
+}
+
 extern "C" const char *tpp_last_error_string(void) { return tpp::g_err; }
 extern "C" int tpp_version(void) { return (1 << 16) | 0; }

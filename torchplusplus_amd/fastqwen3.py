@@ -29,8 +29,10 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from torchplusplus_amd import prepare_device
 from torchplusplus_amd._native import ext as _ext
 from torchplusplus_amd.attention.gqa import GroupedQueryAttention
+from torchplusplus_amd.dlops.derived import DerivedWeight, attach
 from torchplusplus_amd.dlops.linear import (GEMV_MAX_ROWS, LinearSILU, interleave_gate_up,
                                              linear, swiglu)
 from torchplusplus_amd.dlops.normalization import RmsNormFused
@@ -39,6 +41,18 @@ from torchplusplus_amd.llmops.kvcache import KVCache
 from torchplusplus_amd.llmops.llm import LLMInference
 
 _C = _ext()
+
+
+def check_ffn_decode(like: torch.Tensor) -> None:
+    """Raise if a one-launch decode FFN on `like`'s device gave up waiting for
+    its workgroups since the last check (it needs all 256 resident at once;
+    its output is then wrong). Clears the flag and the workspace counters.
+    Synchronises the current stream."""
+    if _C.ffn_decode_sync_errors(like):
+        raise RuntimeError(
+            "ffn_decode: a one-launch decode FFN gave up waiting for its 256 workgroups (not all "
+            "were resident at once, e.g. other work held CUs), so tokens decoded since the last "
+            "check are wrong; the workspace was reset, decode again")
 
 
 @dataclass
@@ -65,24 +79,24 @@ class QwenConfig_float16(QwenConfig):  # noqa: N801  (reference name)
 
 class FFN(nn.Module):
     """SwiGLU FFN: linear_layer2(silu(fused_linear_layer1(x)) * linear_layerP(x)).
-    Runs as one fused gate/up kernel (weights interleaved on first use; call
-    refresh_fused_weights() after changing them) plus the down projection."""
+    Runs as one fused gate/up kernel plus the down projection. The gate/up
+    weights are interleaved on first use and again whenever either changes
+    (load_state_dict, in-place edits)."""
 
     def __init__(self, in_dim: int, hidden_dim: int, dtype=torch.float16, device=None):
         super().__init__()
         self.fused_linear_layer1 = LinearSILU(in_dim, hidden_dim, dtype=dtype, device=device)
         self.linear_layerP = nn.Linear(in_dim, hidden_dim, bias=False, dtype=dtype, device=device)
         self.linear_layer2 = nn.Linear(hidden_dim, in_dim, bias=False, dtype=dtype, device=device)
-        self._w_gu = None
+        self._w_gu = attach(self, DerivedWeight(interleave_gate_up))
 
     def refresh_fused_weights(self):
-        with torch.no_grad():
-            self._w_gu = interleave_gate_up(self.fused_linear_layer1.weight, self.linear_layerP.weight)
+        """Force a rebuild of the interleaved gate/up weight."""
+        self._w_gu.invalidate()
+        self.w_gu()
 
     def w_gu(self) -> torch.Tensor:
-        if self._w_gu is None or self._w_gu.device != self.linear_layerP.weight.device:
-            self.refresh_fused_weights()
-        return self._w_gu
+        return self._w_gu.get(self.fused_linear_layer1.weight, self.linear_layerP.weight)
 
     def forward(self, x):
         return linear(swiglu(x, self.w_gu()), self.linear_layer2.weight)
@@ -137,6 +151,10 @@ class FastQwen3(LLMInference):
         for blk in self.transformer_blocs:
             blk.attn.refresh_fused_weights()
             blk.ffn.refresh_fused_weights()
+
+    def check_device_errors(self):
+        if self.out_head.weight.is_cuda:
+            check_ffn_decode(self.out_head.weight)
 
     def get_num_layers(self) -> int:
         return self.cfg.n_layers
@@ -238,7 +256,10 @@ class GreedyDecoder:
             c.cache_len = max(c.cache_len, position)
 
     def capture(self):
-        """Warm up once on a side stream, restore the state, then capture."""
+        """Run the device checks, warm up once on a side stream (creating the
+        kernels' workspaces outside the capture), restore the state, then
+        capture."""
+        prepare_device(self.ids.device)
         saved = (self.ids.clone(), self.resid.clone(), self.positions.clone(),
                  self.seqlens.clone())
         s = torch.cuda.Stream()
@@ -273,4 +294,6 @@ class GreedyDecoder:
             out[:, t] = self.ids[:, 0]
         for c in self.caches:
             c.cache_len = position + n_steps
+        if n_steps > 0:
+            check_ffn_decode(self.ids)
         return out

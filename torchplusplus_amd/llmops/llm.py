@@ -110,6 +110,11 @@ class LLMInference(nn.Module, ABC):
             return self.sample_top_p(logits, top_p, temperature)
         raise ValueError(f"Unknown sampling strategy: {strategy}")
 
+    def check_device_errors(self):
+        """Raise if the device reported a failed launch during the last
+        generation (models with kernels that can detect one override this;
+        called once at the end of generate(), where it synchronises)."""
+
     def _should_stop(self, token, stop_token_ids: List[int], eos_token_id: Optional[int]) -> bool:
         """True when every sequence of the batch produced EOS or a stop token."""
         ids = list(stop_token_ids) + ([eos_token_id] if eos_token_id is not None else [])
@@ -137,16 +142,17 @@ class LLMInference(nn.Module, ABC):
         if stream and stream_callback:
             stream_callback(next_token)
         generated = [next_token]
-        if self._should_stop(next_token, stop_token_ids, eos_token_id):
-            return torch.cat([input_ids] + generated, dim=1)
-        for i in range(max_new_token - 1):
-            logits = self.forward_impl(next_token, self.kv_cache_array, seq_len + i)
-            next_token = self._sample_token(logits[:, -1, :], temp, top_p, top_k, sampling_strategy)
-            if stream and stream_callback:
-                stream_callback(next_token)
-            generated.append(next_token)
-            if self._should_stop(next_token, stop_token_ids, eos_token_id):
-                break
+        if not self._should_stop(next_token, stop_token_ids, eos_token_id):
+            for i in range(max_new_token - 1):
+                logits = self.forward_impl(next_token, self.kv_cache_array, seq_len + i)
+                next_token = self._sample_token(logits[:, -1, :], temp, top_p, top_k,
+                                                sampling_strategy)
+                if stream and stream_callback:
+                    stream_callback(next_token)
+                generated.append(next_token)
+                if self._should_stop(next_token, stop_token_ids, eos_token_id):
+                    break
+        self.check_device_errors()
         return torch.cat([input_ids] + generated, dim=1)
 
     def get_cache_info(self) -> dict:
