@@ -325,6 +325,43 @@ int tpp_attn_decode_fused(const void *qkv, const void *q_norm_w,
                           int dtype, void *workspace, size_t ws_bytes,
                           void *stream);
 
+/* Workspace bytes of tpp_attn_decode_oproj (256-byte aligned, zero-filled
+ * before first use; counters in it are left at zero by every call; it may be
+ * shared with tpp_attn_decode / tpp_attn_decode_fused calls, in order). */
+size_t tpp_attn_decode_oproj_workspace_size(int64_t B, int64_t Hq, int64_t Hkv,
+                                            int64_t D, int64_t Lmax, int64_t E);
+
+/* tpp_attn_decode_fused followed by the attention block's output projection
+ * and residual add (the `x + x_res` after GroupedQueryAttention,
+ * torchpp/attention/gqa.py:128-131 and examples/LLM/fastqwen3.py:107-111):
+ *   o = attention output [B, 1, Hq, D] (contiguous, rounded to T)
+ *   residual[B, E] <- T(residual + T(o W^T)),  W = w_o [E, Hq * D]
+ * For Hkv = 8, D = 128, Hq in {8, 16}, E = 1024, B in {1, 2, 4, 8, 16} on
+ * a 256-CU device whose workgroup placement probe holds (see
+ * tpp_prepare_device) this is ONE launch: the XCD of KV head x computes the
+ * projection over its heads' K slice and the 8 slices are summed in a fixed
+ * order; that launch needs all 256 workgroups resident at once and reports a
+ * failed wait through tpp_attn_decode_oproj_sync_errors. Otherwise it is
+ * tpp_attn_decode_fused + tpp_gemv_fused (two launches). `o` is always
+ * written. No counterpart in the reference, which runs the projection as a
+ * separate nn.Linear. */
+int tpp_attn_decode_oproj(const void *qkv, const void *q_norm_w,
+                          const void *k_norm_w, const void *cos,
+                          const void *sin, int64_t ctx, int cs_dtype, float eps,
+                          void *k_cache, void *v_cache, void *o,
+                          const int64_t *k_strides, const int64_t *v_strides,
+                          const int32_t *seqlens, const void *w_o,
+                          void *residual, int64_t B, int64_t Hq, int64_t Hkv,
+                          int64_t D, int64_t Lmax, int64_t E,
+                          float softmax_scale, int window_left, int dtype,
+                          void *workspace, size_t ws_bytes, void *stream);
+
+/* *out = nonzero if a one-launch tpp_attn_decode_oproj on this workspace
+ * gave up waiting for its workgroups since the last call (its residual
+ * update is WRONG); the flag and the counters are then zeroed. Same calling
+ * rules as tpp_ffn_decode_sync_errors. */
+int tpp_attn_decode_oproj_sync_errors(void *workspace, int *out, void *stream);
+
 /* ---- sampling ------------------------------------------------------------ */
 
 /* Greedy sampling: out[b] = argmax_n x[b, n] for x [B, ldx] (first index of

@@ -280,3 +280,179 @@ def test_decode_fused_model_shape_split_merge(dev, lens):
     got2 = C.attn_decode_fused(qkv.to(dev), qw.to(dev), kw.to(dev), cos.to(dev), sin.to(dev), 1e-6,
                                kd, vd, seqlens.to(dev))
     assert torch.equal(got, got2), "repeated call differs"
+
+
+def _oproj_inputs(B, hq, hkv, Lmax, lens, seed, E=1024, D=128):
+    g = torch.Generator().manual_seed(seed)
+    qkv = torch.randn(B, 1, (hq + 2 * hkv) * D, generator=g).bfloat16()
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    cos, sin = oracle.compute_rope_params(D, 1e6, Lmax + 1)
+    kc = torch.randn(B, hkv, Lmax, D, generator=g).bfloat16()
+    vc = torch.randn(B, hkv, Lmax, D, generator=g).bfloat16()
+    w_o = (0.02 * torch.randn(E, hq * D, generator=g)).bfloat16()
+    resid = torch.randn(B, 1, E, generator=g).bfloat16()
+    return qkv, qw, kw, cos, sin, kc, vc, w_o, resid, torch.tensor(lens, dtype=torch.int32)
+
+
+def _oproj_oracle(qkv, qw, kw, cos, sin, kc, vc, w_o, resid, seqlens, hq, hkv):
+    """The reference block's attention half for one new token: QK-norm, RoPE,
+    cache append, attention (torchpp/attention/gqa.py:90-128), the output
+    projection and the residual add (examples/LLM/fastqwen3.py:107-111), each
+    op's output rounded to the model dtype."""
+    o, k_ref, v_ref = _fused_decode_oracle(qkv, hq, hkv, qw, kw, cos, sin, kc, vc, seqlens - 1)
+    B = o.shape[0]
+    proj = oracle.gemv(o.reshape(B, -1), w_o)
+    return o, (resid.float() + proj.float().view(B, 1, -1)).to(resid.dtype), k_ref, v_ref
+
+
+def _oproj_capi(o, kd, vd, qkv, qw, kw, cos, sin, seqlens, w_o, resid, ws):
+    import ctypes
+
+    from torchplusplus_amd._native import lib
+
+    B, hkv, Lmax, D = kd.shape
+    hq = o.shape[2]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    ks = (ctypes.c_int64 * 3)(kd.stride(0), kd.stride(2), kd.stride(1))
+    vs = (ctypes.c_int64 * 3)(vd.stride(0), vd.stride(2), vd.stride(1))
+    L = lib()
+    rc = L.tpp_attn_decode_oproj(
+        P(qkv), P(qw), P(kw), P(cos), P(sin), ctypes.c_int64(cos.shape[0]), ctypes.c_int(0),
+        ctypes.c_float(1e-6), P(kd), P(vd), P(o), ks, vs, P(seqlens), P(w_o), P(resid),
+        ctypes.c_int64(B), ctypes.c_int64(hq), ctypes.c_int64(hkv), ctypes.c_int64(D),
+        ctypes.c_int64(Lmax), ctypes.c_int64(w_o.shape[0]), ctypes.c_float(0.0), ctypes.c_int(-1),
+        ctypes.c_int(1), P(ws), ctypes.c_size_t(ws.numel()),
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, L.tpp_last_error_string()
+
+
+@pytest.mark.parametrize("lens", [[2049] * 8, [2068] * 8, [2068, 2049, 2060, 1921, 1920, 641, 640, 1]],
+                         ids=["L2049", "L2068", "ragged"])
+def test_decode_oproj_model_shape(dev, lens):
+    """Decode attention with the output projection and residual add folded in
+    (one launch) at the benchmark shape: batch 8, 16/8 heads, a 2069-row
+    cache, W_o [1024, 2048]. Attention output, appended K/V and the updated
+    residual against the oracle; the same launch through the C ABI on a
+    workspace whose partial-projection region starts as NaN must leave it
+    finite (the one-launch path ran, not the two-launch fallback) and give
+    the binding's residual bit for bit."""
+    import ctypes
+
+    import torchplusplus_amd
+    from torchplusplus_amd._native import ext, lib
+
+    info = torchplusplus_amd.prepare_device(dev)
+    if info["cu_count"] != 256:
+        pytest.skip(f"the one-launch path needs 256 CUs, device has {info['cu_count']}")
+    assert info["xcd_local"]
+    C = ext()
+    B, hq, hkv, D, Lmax, E = 8, 16, 8, 128, 2069, 1024
+    qkv, qw, kw, cos, sin, kc, vc, w_o, resid, seqlens = _oproj_inputs(B, hq, hkv, Lmax, lens, 22)
+    e_o, e_res, k_ref, v_ref = _oproj_oracle(qkv, qw, kw, cos, sin, kc, vc, w_o, resid, seqlens,
+                                             hq, hkv)
+    dq = [t.to(dev) for t in (qkv, qw, kw, cos, sin, seqlens, w_o)]
+    kd, vd, rd = kc.to(dev), vc.to(dev), resid.to(dev)
+    o = C.attn_decode_oproj(dq[0], dq[1], dq[2], dq[3], dq[4], 1e-6, kd, vd, dq[5], dq[6], rd)
+    close(kd.cpu(), k_ref, what="oproj decode: appended K")
+    assert torch.equal(vd.cpu(), v_ref), "oproj decode: appended V"
+    close(o, e_o, what="oproj decode: attention output vs oracle")
+    close(rd, e_res, what="oproj decode: residual vs oracle")
+    assert C.attn_decode_sync_errors(rd) == 0
+    # C ABI on a NaN-filled workspace
+    f = lib().tpp_attn_decode_oproj_workspace_size
+    f.restype = ctypes.c_size_t
+    need = f(*(ctypes.c_int64(v) for v in (B, hq, hkv, D, Lmax, E)))
+    part_off = 65536 + B * hq * 4 * (D + 32) * 4
+    assert need == part_off + 8 * B * E * 4
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=dev)
+    ws[:65536] = 0
+    kd2, vd2, rd2 = kc.to(dev), vc.to(dev), resid.to(dev)
+    o2 = torch.empty_like(o)
+    _oproj_capi(o2, kd2, vd2, dq[0], dq[1], dq[2], dq[3], dq[4], dq[5], dq[6], rd2, ws)
+    torch.cuda.synchronize()
+    part = ws[part_off:].view(torch.float32)
+    assert torch.isfinite(part).all(), "partial projections not written: the fallback ran"
+    assert torch.equal(rd2, rd) and torch.equal(o2, o)
+    assert int(ws[:65536].view(torch.int32).abs().sum()) == 0, "counters not back at zero"
+
+
+@pytest.mark.parametrize("B,hq", [(1, 16), (2, 16), (4, 16), (16, 16), (8, 8), (16, 8)])
+def test_decode_oproj_batches_and_groups(dev, B, hq):
+    """The one-launch path at every batch it takes (32 / B splits per
+    sequence; B = 1 leaves most splits without a key) and with one query head
+    per KV head (G = 1, K slice 128), ragged lengths, vs the oracle."""
+    hkv, Lmax = 8, 700
+    g = torch.Generator().manual_seed(B * 31 + hq)
+    lens = torch.randint(1, Lmax + 1, (B,), generator=g).tolist()
+    qkv, qw, kw, cos, sin, kc, vc, w_o, resid, seqlens = _oproj_inputs(B, hq, hkv, Lmax, lens, 23 + B)
+    e_o, e_res, _, _ = _oproj_oracle(qkv, qw, kw, cos, sin, kc, vc, w_o, resid, seqlens, hq, hkv)
+    from torchplusplus_amd._native import ext
+
+    C = ext()
+    rd = resid.to(dev)
+    o = C.attn_decode_oproj(qkv.to(dev), qw.to(dev), kw.to(dev), cos.to(dev), sin.to(dev), 1e-6,
+                            kc.to(dev), vc.to(dev), seqlens.to(dev), w_o.to(dev), rd)
+    close(o, e_o, what=f"oproj decode B={B} Hq={hq}: attention output")
+    close(rd, e_res, what=f"oproj decode B={B} Hq={hq}: residual")
+
+
+def test_decode_oproj_unfolded_shape(dev):
+    """Hkv = 4 (not one KV head per XCD): the entry point runs the fused
+    decode attention and the projection GEMV; same results vs the oracle."""
+    B, hq, hkv, Lmax = 3, 8, 4, 300
+    qkv, qw, kw, cos, sin, kc, vc, w_o, resid, seqlens = _oproj_inputs(
+        B, hq, hkv, Lmax, [300, 17, 1], 24, E=512)
+    e_o, e_res, _, _ = _oproj_oracle(qkv, qw, kw, cos, sin, kc, vc, w_o, resid, seqlens, hq, hkv)
+    from torchplusplus_amd._native import ext
+
+    rd = resid.to(dev)
+    o = ext().attn_decode_oproj(qkv.to(dev), qw.to(dev), kw.to(dev), cos.to(dev), sin.to(dev),
+                                1e-6, kc.to(dev), vc.to(dev), seqlens.to(dev), w_o.to(dev), rd)
+    close(o, e_o, what="unfolded oproj decode: attention output")
+    close(rd, e_res, what="unfolded oproj decode: residual")
+
+
+def test_decode_oproj_graph_replays_over_layers(dev):
+    """28 launches over distinct caches and weights captured in one graph (as
+    the decode step does), replayed three times with eager work in between:
+    every replay equals the eager run (counters back at zero after every
+    launch), and no launch gave up waiting."""
+    from torchplusplus_amd._native import ext
+
+    C = ext()
+    B, hq, hkv, D, Lmax, E, NL = 8, 16, 8, 128, 640, 1024, 28
+    g = torch.Generator(device=dev).manual_seed(25)
+    cos, sin = (t.to(dev) for t in oracle.compute_rope_params(D, 1e6, Lmax + 1))
+    layers = []
+    for _ in range(NL):
+        layers.append(((0.5 * torch.randn(B, 1, (hq + 2 * hkv) * D, generator=g, device=dev)).bfloat16(),
+                       torch.randn(B, hkv, Lmax, D, generator=g, device=dev).bfloat16(),
+                       torch.randn(B, hkv, Lmax, D, generator=g, device=dev).bfloat16(),
+                       (0.02 * torch.randn(E, hq * D, generator=g, device=dev)).bfloat16()))
+    seqlens = torch.randint(400, Lmax + 1, (B,), generator=g, device=dev, dtype=torch.int32)
+    start = torch.randn(B, 1, E, generator=g, device=dev).bfloat16()
+    resid = start.clone()
+
+    def run():
+        for qkv, kc, vc, w in layers:
+            C.attn_decode_oproj(qkv, None, None, cos, sin, 1e-6, kc, vc, seqlens, w, resid)
+
+    run()
+    want = resid.clone()
+    resid.copy_(start)
+    run()
+    assert torch.equal(resid, want), "eager runs differ"
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    resid.copy_(start)
+    with torch.cuda.graph(graph, stream=s):
+        run()
+    for rep in range(3):
+        resid.copy_(start)
+        graph.replay()
+        _ = torch.randn(1000, device=dev).sum()
+        torch.cuda.synchronize()
+        assert torch.equal(resid, want), f"replay {rep} differs from eager"
+    assert C.attn_decode_sync_errors(resid) == 0

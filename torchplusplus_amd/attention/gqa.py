@@ -103,6 +103,29 @@ class GroupedQueryAttention(nn.Module):
                                     self.k_norm.weight if self.k_norm is not None else None,
                                     cos, sin, eps, k_cache, v_cache, seqlens)
 
+    def decode_oproj(self, qkv, cos, sin, k_cache, v_cache, seqlens, residual):
+        """decode_fused, then the output projection with the residual add:
+        residual [B, 1, d_in] <- residual + out_projection(attention output),
+        in place (one launch at the Qwen3-0.6B decode shape); returns the
+        attention output [B, 1, Hq, D]."""
+        eps = self.q_norm.eps if self.q_norm is not None and self.q_norm.eps is not None else 1e-6
+        return _C.attn_decode_oproj(qkv, self.q_norm.weight if self.q_norm is not None else None,
+                                    self.k_norm.weight if self.k_norm is not None else None,
+                                    cos, sin, eps, k_cache, v_cache, seqlens,
+                                    self.out_projection.weight, residual)
+
+    def attend_oproj(self, qkv, cos, sin, kv_cache: KVCache, cache_pos: Optional[int],
+                     residual: torch.Tensor) -> None:
+        """One new token per sequence through the cache: steps 2-4 with the
+        residual add, residual [B, 1, d_in] updated in place."""
+        bs = qkv.shape[0]
+        start = kv_cache.cache_len if cache_pos is None else int(cache_pos)
+        kv_cache.ensure(bs, start + 1)
+        seqlens = _positions(bs, start + 1, qkv.device)
+        kv_cache.cache_len = max(kv_cache.cache_len, start + 1)
+        self.decode_oproj(qkv, cos, sin, kv_cache.k_cache[:bs], kv_cache.v_cache[:bs], seqlens,
+                          residual)
+
     def attend(self, qkv, cos, sin, kv_cache: Optional[KVCache] = None,
                cache_pos: Optional[int] = None) -> torch.Tensor:
         """Steps 2-3: rope/cache the projected qkv and attend; returns the

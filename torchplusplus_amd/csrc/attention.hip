@@ -63,6 +63,16 @@ struct DecodeFuse {
   float eps;
 };
 
+// Output projection + residual add folded into the decode attention (the
+// OP instantiation): residual[B, E] <- T(residual + T(T(o) W^T)).
+struct DecodeOproj {
+  const void *w; // [E, Hq * D] (nn.Linear layout)
+  void *resid;   // [B, E]
+  int *ctr;      // counter region (XCD arrival / departure, chunk counters, error flag)
+  float *part;   // [8][B][E] fp32 per-XCD partial projections
+  int E;
+};
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kKvTile = 64;
 // 32-query groups per prefill wave (each K / V^T fragment read from LDS feeds
@@ -640,7 +650,9 @@ constexpr int kDecMaxSplit = 256;
 #define TPP_DEC_INLINE_MERGE 1
 #endif
 constexpr bool kDecInlineMerge = TPP_DEC_INLINE_MERGE;
-constexpr int64_t kDecCounterBytes = 65536; // arrival counters region of the workspace
+constexpr int64_t kDecCounterBytes = 65536; // counters region at the start of the workspace:
+constexpr int64_t kDecOpCtrOffset = 32768;  // per-pair arrival counters below, the folded
+                                            // projection's counters from here
 #ifndef TPP_DEC_WAVES
 #define TPP_DEC_WAVES 2048
 #endif
@@ -693,18 +705,217 @@ __device__ __forceinline__ void cs_vals(u32x4 lo, u32x4 hi, int cs_dtype, float 
   }
 }
 
+// Folded output projection (OP): one workgroup per CU, 8 XCDs x 32, the XCD
+// of a workgroup = its KV head (Hkv = 8), so XCD x holds every split of every
+// sequence for query heads x G .. x G + G - 1, i.e. the K slice
+// [x G D, (x + 1) G D) of the projection. Its workgroup j owns output
+// columns [32 j, 32 j + 32). Constants of that layout:
+constexpr int kOpXcds = 8, kOpPerXcd = 32, kOpCols = 32;
+constexpr unsigned kOpSpinLimit = 1u << 20;
+// counter region (ints, each counter on its own 128-byte line) at
+// kDecOpCtrOffset of the workspace: arrive[8], depart[8], chunk[32], err
+constexpr int kOpArrive = 0, kOpDepart = 8 * 32, kOpChunk = 16 * 32, kOpErr = 48 * 32;
+
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16x32(typename VecT<T>::v8 a, typename VecT<T>::v8 b, f32x4 c) {
+  if constexpr (__is_same(T, bf16))
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// End of the OP kernel, after this workgroup published its split partial:
+//  1. XCD-local sync: the workgroup counts itself in and waits until all 32
+//     workgroups of its XCD (every split of every sequence for the XCD's KV
+//     head) have published; the partials then sit in this XCD's L2. The wait
+//     is bounded: if the workgroups were not all resident it gives up, sets
+//     the error flag and the output is wrong (flagged).
+//  2. Every workgroup merges the splits of all B sequences for the XCD's G
+//     heads into LDS (the attention output, rounded to T like the unfused
+//     path's output tensor), and workgroup j < B also stores sequence j's
+//     rows to the output tensor.
+//  3. Partial projection of output columns [32 j, 32 j + 32) over the XCD's
+//     K slice with v_mfma_f32_16x16x32 (batch rows padded to 16), written
+//     through to memory as fp32.
+//  4. An agent-scope counter per column chunk finds the chunk's last XCD,
+//     which sums the 8 partials in XCD order (fixed: bit-reproducible) and
+//     updates the residual: T(residual + T(sum)).
 template <typename T, int D, int G, int NW>
+__device__ __forceinline__ void attn_decode_oproj_tail(const AttnArgs &p, const float *__restrict__ ws_o,
+                                                       int nsplit, const DecodeOproj &op,
+                                                       const T *s_w, T *s_o, f32x4 (*s_red)[64]) {
+  typedef typename VecT<T>::v8 V8;
+  constexpr int KO = G * D, UPR = KO / 8;
+  const int lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int x = blockIdx.x % kOpXcds, jb = blockIdx.x / kOpXcds;
+  const int B = p.B, E = op.E;
+  int *arrive = op.ctr + kOpArrive + x * 32;
+  int *depart = op.ctr + kOpDepart + x * 32;
+  int *chunkc = op.ctr + kOpChunk + jb * 32;
+  int *err = op.ctr + kOpErr;
+  T *resid = (T *)op.resid;
+  __shared__ int s_last;
+  // residual values of this workgroup's column chunk (used if it is the
+  // chunk's last XCD), requested before the waits below
+  const int e = threadIdx.x; // blockDim.x == 512 >= 16 * 32
+  const int rb = e / kOpCols < B ? e / kOpCols : 0;
+  const T rres = resid[(int64_t)rb * E + kOpCols * jb + e % kOpCols];
+
+  // ---- 1. XCD-local sync (the partial stores and the weight DMA are done:
+  // vmcnt(0); the counter lives in this XCD's L2, polled with an atomic add
+  // of 0 from an asm move so the compiler keeps it an atomic)
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned n = 0;
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    while (__hip_atomic_fetch_add(arrive, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < kOpPerXcd) {
+      if (++n > kOpSpinLimit) {
+        __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    // the XCD's last workgroup past the wait resets both counters
+    if (__hip_atomic_fetch_add(depart, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        kOpPerXcd - 1) {
+      __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(depart, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+
+  // ---- 2. merge the splits: item = (batch row, head, 4 columns); rows past
+  // B are zero (MFMA padding). Each split slot is D outputs, m, l, padding.
+  for (int it = threadIdx.x; it < 16 * G * (D / 4); it += 64 * NW) {
+    const int d4 = it % (D / 4), gi = (it / (D / 4)) % G, bb = it / (D / 4 * G);
+    float r[4] = {0.f, 0.f, 0.f, 0.f};
+    if (bb < B) {
+      const float *sl = ws_o + ((int64_t)bb * p.Hq + x * G + gi) * nsplit * (D + 32);
+      constexpr int MG = 8;
+      float mu = -INFINITY, ls = 0.f, os[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int s0 = 0; s0 < nsplit; s0 += MG) {
+        float mv[MG], lv[MG];
+        f32x4 ov[MG];
+#pragma unroll
+        for (int jj = 0; jj < MG; ++jj) {
+          const int sp = s0 + jj < nsplit ? s0 + jj : nsplit - 1;
+          const float *q = sl + (int64_t)sp * (D + 32);
+          mv[jj] = q[D];
+          lv[jj] = q[D + 1];
+          ov[jj] = *reinterpret_cast<const f32x4 *>(q + 4 * d4);
+        }
+        float mx = mu;
+#pragma unroll
+        for (int jj = 0; jj < MG; ++jj)
+          if (s0 + jj < nsplit) mx = fmaxf(mx, mv[jj]);
+        const float mn = mx == -INFINITY ? 0.f : mx;
+        const float a = mu == -INFINITY ? 0.f : exp2f(mu - mn);
+        ls *= a;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) os[c] *= a;
+#pragma unroll
+        for (int jj = 0; jj < MG; ++jj) {
+          const float wgt = s0 + jj < nsplit ? exp2f(mv[jj] - mn) : 0.f;
+          ls += wgt * lv[jj];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) os[c] += wgt * ov[jj][c];
+        }
+        mu = mx;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) r[c] = ls > 0.f ? os[c] / ls : 0.f;
+    }
+    T tv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) tv[c] = from_f32<T>(r[c]);
+    T *so = s_o + bb * (KO + 8) + gi * D + 4 * d4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) so[c] = tv[c];
+    if (bb < B && bb == jb) {
+      T *o = (T *)p.o + (int64_t)bb * p.o_sb + (int64_t)(x * G + gi) * p.o_sh + 4 * d4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = tv[c];
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. partial projection: waves 0-3 output columns 32 j .. + 15,
+  // waves 4-7 the next 16; wave w & 3 takes K steps (w & 3) G .. + G - 1 of 32
+  const int t = w >> 2;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int ks = (w & 3) * G + i;
+    const int gu = ks * 4 + (lane >> 4);          // 16-byte unit of K
+    const int wr = 16 * t + (lane & 15);          // weight row of the tile
+    const V8 a = *reinterpret_cast<const V8 *>(s_o + (lane & 15) * (KO + 8) + gu * 8);
+    const V8 bw = *reinterpret_cast<const V8 *>(s_w + wr * KO + (gu ^ (wr & (UPR - 1))) * 8);
+    acc = mfma16x32<T>(a, bw, acc);
+  }
+  s_red[w][lane] = acc;
+  __syncthreads();
+  if ((w & 3) == 0) {
+    f32x4 sum = s_red[w][lane];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) sum += s_red[w + i][lane];
+    // D layout: lane -> column lane & 15, batch rows 4 (lane >> 4) + i
+    const int n = kOpCols * jb + 16 * t + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = 4 * (lane >> 4) + i;
+      if (b < B)
+        __hip_atomic_store(op.part + ((int64_t)x * B + b) * E + n, sum[i], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // ---- 4. partial written through (vmcnt(0)); count this XCD in for the chunk
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(chunkc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == kOpXcds - 1;
+    if (old == kOpXcds - 1) __hip_atomic_store(chunkc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last || e >= B * kOpCols) return;
+  const int b = e / kOpCols, n = kOpCols * jb + e % kOpCols;
+  float v[kOpXcds];
+#pragma unroll
+  for (int xx = 0; xx < kOpXcds; ++xx)
+    v[xx] = __hip_atomic_load(op.part + ((int64_t)xx * B + b) * E + n, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+  float sum = 0.f;
+#pragma unroll
+  for (int xx = 0; xx < kOpXcds; ++xx) sum += v[xx];
+  resid[(int64_t)b * E + n] = from_f32<T>(to_f32(rres) + to_f32(from_f32<T>(sum)));
+}
+
+template <typename T, int D, int G, int NW, bool OP = false>
 __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const int *__restrict__ seqlens,
                                                               int fixed_len, float *__restrict__ ws_o,
                                                               float *__restrict__ ws_ml, int chunk,
                                                               int nsplit, DecodeFuse fz,
-                                                              int *__restrict__ counters) {
+                                                              int *__restrict__ counters,
+                                                              DecodeOproj op) {
   typedef typename VecT<T>::v8 V8;
   constexpr int LPK = D / 8;        // lanes per key
   constexpr int KPW = kWave / LPK;  // keys per wave pass
   constexpr int U = kDecU;
   __shared__ float red_m[NW][G], red_l[NW][G];
   __shared__ float red_o[NW][G][D];
+  // OP: the workgroup's [32 x G D] projection weight tile (LDS-DMA at kernel
+  // start, 16-byte units of a row XOR-swizzled by the row), the merged
+  // attention output of the XCD's heads for 16 (padded) batch rows, and the
+  // cross-wave reduction of the projection
+  constexpr int KO = G * D;        // projection K slice of an XCD
+  constexpr int UPR = KO / 8;      // 16-byte units per weight row
+  __shared__ __attribute__((aligned(16))) T s_w[OP ? kOpCols * KO : 8];
+  __shared__ __attribute__((aligned(16))) T s_o[OP ? 16 * (KO + 8) : 8];
+  __shared__ f32x4 s_red[OP ? NW : 1][64];
+  static_assert(!OP || (D == 128 && NW == 8 && G <= 2), "folded projection: D 128, 8 waves, G <= 2");
 
   // w through readfirstlane: the compiler then knows it (and every key index
   // derived from it) is wave-uniform, so the key loop's exits are scalar
@@ -748,6 +959,24 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
   V8 k0[U], v0[U], k1[U], v1[U], k2[U], v2[U];
   load_batch(first, p.Sk - 1, k0, v0);
   load_batch(first + STRIDE, p.Sk - 1, k1, v1);
+  if constexpr (OP) {
+    // the projection weight tile W[32 j .. 32 j + 31][x G D .. + G D) by
+    // LDS-DMA (1 KB per wave instruction). Issued before the prologue loads,
+    // whose first use waits for every load in flight anyway, so the compiler's
+    // counted waits of the key loop are not disturbed by it.
+    const int jb = blockIdx.x / kOpXcds;
+    const T *wsrc = (const T *)op.w + (int64_t)(kOpCols * jb) * (p.Hq * D) + (int64_t)hk * KO;
+    constexpr int NQ = kOpCols * KO * (int)sizeof(T) / (NW * 1024); // instructions per wave
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int unit = (w * NQ + q) * 64 + lane; // LDS 16-byte unit
+      const int r = unit / UPR, lu = unit % UPR;
+      const int gu = lu ^ (r & (UPR - 1));       // global unit stored at LDS unit lu
+      __builtin_amdgcn_global_load_lds(
+          (const void *)(wsrc + (int64_t)r * (p.Hq * D) + gu * 8),
+          (__attribute__((address_space(3))) void *)(s_w + (w * NQ + q) * 64 * 8), 16, 0, 0);
+    }
+  }
 
   const int Lraw = seqlens ? seqlens[b] : fixed_len;
   const int L = Lraw < p.Sk ? (Lraw > 0 ? Lraw : 0) : p.Sk; // never read past the cache
@@ -1003,6 +1232,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
       if (d == 0) ws_ml[slot * 2] = mx, ws_ml[slot * 2 + 1] = ls;
     }
   }
+  if constexpr (OP) {
+    attn_decode_oproj_tail<T, D, G, NW>(p, ws_o, nsplit, op, s_w, s_o, s_red);
+    return;
+  }
   if (!counters || nsplit == 1) return;
   // The last block of the pair to finish merges the splits. Every thread
   // waits for its partial stores to reach L2 (an explicit vmcnt(0): the
@@ -1208,7 +1441,7 @@ static DecodePlan plan_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
   pl.chunk = (int)chunk;
   pl.nsplit = (int)((Lmax + chunk - 1) / chunk);
   if (pl.nsplit < 1) pl.nsplit = 1;
-  pl.inline_merge = pl.nsplit > 1 && pairs % 8 == 0 && pairs * (int64_t)sizeof(int) <= kDecCounterBytes &&
+  pl.inline_merge = pl.nsplit > 1 && pairs % 8 == 0 && pairs * (int64_t)sizeof(int) <= kDecOpCtrOffset &&
                     kDecInlineMerge;
   const size_t slots = (size_t)(B * Hq * pl.nsplit);
   if (pl.nsplit == 1) {
@@ -1230,17 +1463,20 @@ template <typename T, int D, int G>
 static void launch_decode_g(const AttnArgs &a, dim3 grid, const int *seqlens, int L, float *ws_o,
                             float *ws_ml, int *counters, const DecodePlan &pl, const DecodeFuse &fz,
                             hipStream_t st) {
+  const DecodeOproj none{};
   if constexpr (G <= 2) {
     if (pl.nw == kDecBigNW) {
-      attn_decode_kernel<T, D, G, kDecBigNW><<<grid, dim3(64 * kDecBigNW), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
-                                                                 pl.chunk, pl.nsplit, fz, counters);
+      attn_decode_kernel<T, D, G, kDecBigNW><<<grid, dim3(64 * kDecBigNW), 0, st>>>(
+          a, seqlens, L, ws_o, ws_ml, pl.chunk, pl.nsplit, fz, counters, none);
     } else {
       attn_decode_kernel<T, D, G, 4><<<grid, dim3(256), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
-                                                                 pl.chunk, pl.nsplit, fz, counters);
+                                                                 pl.chunk, pl.nsplit, fz, counters,
+                                                                 none);
     }
   } else
     attn_decode_kernel<T, D, G, 4><<<grid, dim3(256), 0, st>>>(a, seqlens, L, ws_o, ws_ml,
-                                                               pl.chunk, pl.nsplit, fz, counters);
+                                                               pl.chunk, pl.nsplit, fz, counters,
+                                                               none);
   if (pl.nsplit > 1 && !counters)
     attn_decode_merge_kernel<T, D, G><<<dim3(a.Hkv, a.B), dim3(G * D), 0, st>>>(
         a, ws_o, ws_ml, pl.nsplit);
@@ -1476,4 +1712,133 @@ extern "C" int tpp_attn_decode_fused(const void *qkv, const void *q_norm_w, cons
                          Lmax, Hq, Hkv, D, softmax_scale, window_left < 0 ? -1 : window_left, 0);
   DecodeFuse fz{qkv, q_norm_w, k_norm_w, cos, sin, cs_dtype, (int)ctx, eps};
   return decode_impl(name, a, D, Lmax, seqlens, fz, dtype, workspace, ws_bytes, stream);
+}
+
+// ---- decode attention + output projection + residual add -------------------
+// The OP kernel's plan: one workgroup per CU (Hkv = 8 KV heads x B sequences
+// x 32 / B splits = 256), splits in whole 128-key load batches (trailing
+// splits may hold no key). Workspace: the counters region (the projection's
+// counters at kDecOpCtrOffset), the split partial slots, then the fp32
+// per-XCD partial projections [8][B][E].
+static bool oproj_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t E) {
+  return Hkv == kOpXcds && D == 128 && (Hq == 8 || Hq == 16) && E == kOpPerXcd * kOpCols &&
+         (B == 1 || B == 2 || B == 4 || B == 8 || B == 16);
+}
+
+struct OprojPlan {
+  int nsplit, chunk;
+  size_t part_off, ws_bytes;
+};
+
+static OprojPlan plan_oproj(int64_t B, int64_t Hq, int64_t D, int64_t Lmax, int64_t E) {
+  OprojPlan pl{};
+  constexpr int64_t stride = kDecBigNW * (kWave / 16) * kDecU; // keys per block-wide batch (D 128)
+  pl.nsplit = (int)(kOpPerXcd / B);
+  int64_t chunk = (Lmax + pl.nsplit - 1) / pl.nsplit;
+  chunk = (chunk + stride - 1) / stride * stride;
+  pl.chunk = (int)chunk;
+  pl.part_off = (size_t)kDecCounterBytes + (size_t)(B * Hq * pl.nsplit) * (size_t)(D + 32) * sizeof(float);
+  pl.ws_bytes = pl.part_off + (size_t)kOpXcds * B * E * sizeof(float);
+  return pl;
+}
+
+extern "C" size_t tpp_attn_decode_oproj_workspace_size(int64_t B, int64_t Hq, int64_t Hkv,
+                                                       int64_t D, int64_t Lmax, int64_t E) {
+  const size_t plain = plan_decode(B, Hq, Hkv, D, Lmax).ws_bytes;
+  if (!oproj_shape(B, Hq, Hkv, D, E) || Lmax < 1) return plain;
+  const size_t op = plan_oproj(B, Hq, D, Lmax, E).ws_bytes;
+  return op > plain ? op : plain;
+}
+
+extern "C" int tpp_attn_decode_oproj(const void *qkv, const void *q_norm_w, const void *k_norm_w,
+                                     const void *cos, const void *sin, int64_t ctx, int cs_dtype,
+                                     float eps, void *k_cache, void *v_cache, void *o,
+                                     const int64_t *k_strides, const int64_t *v_strides,
+                                     const int32_t *seqlens, const void *w_o, void *residual,
+                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t Lmax,
+                                     int64_t E, float softmax_scale, int window_left, int dtype,
+                                     void *workspace, size_t ws_bytes, void *stream) {
+  const char *name = "tpp_attn_decode_oproj";
+  if (!w_o || !residual || !o) return set_error(TPP_E_INVALID, "%s: null pointer argument", name);
+  if (!aligned16(w_o) || !aligned16(residual) || !aligned16(o))
+    return set_error(TPP_E_INVALID, "%s: 16-byte alignment required", name);
+  if (E <= 0 || B <= 0 || B > 16)
+    return set_error(TPP_E_INVALID, "%s: need 1 <= B <= 16 and E > 0", name);
+  const int64_t os[3] = {Hq * D, Hq * D, D}; // o: contiguous [B, 1, Hq, D]
+  hipStream_t st = as_stream(stream);
+  const size_t need = tpp_attn_decode_oproj_workspace_size(B, Hq, Hkv, D, Lmax, E);
+  if (!workspace || ws_bytes < need || (uintptr_t)workspace % 128 != 0)
+    return set_error(TPP_E_WORKSPACE, "%s: 128-byte aligned workspace of %zu bytes required", name,
+                     need);
+  const bool fold = oproj_shape(B, Hq, Hkv, D, E) && half_type(dtype) &&
+                    device_cu_count() == kOpXcds * kOpPerXcd && xcd_grouping_holds(st, true);
+  if (!fold) {
+    // two launches: fused decode attention into o, then the projection GEMV
+    // with the residual add
+    if (int rc = tpp_attn_decode_fused(qkv, q_norm_w, k_norm_w, cos, sin, ctx, cs_dtype, eps,
+                                       k_cache, v_cache, o, k_strides, v_strides, os, seqlens, B,
+                                       Hq, Hkv, D, Lmax, softmax_scale, window_left, dtype,
+                                       workspace, ws_bytes, stream))
+      return rc;
+    return tpp_gemv_fused(o, nullptr, 0.f, w_o, nullptr, residual, B, E, Hq * D, 0, dtype, stream);
+  }
+  if (!k_strides || !v_strides) return set_error(TPP_E_INVALID, "%s: null stride array", name);
+  if (!qkv || !cos || !sin || !seqlens)
+    return set_error(TPP_E_INVALID, "%s: qkv, cos, sin and seqlens are required", name);
+  if (!aligned16(qkv) || !aligned16(cos) || !aligned16(sin) ||
+      (q_norm_w && !aligned16(q_norm_w)) || (k_norm_w && !aligned16(k_norm_w)))
+    return set_error(TPP_E_INVALID, "%s: 16-byte alignment required", name);
+  if (cs_dtype != TPP_F16 && cs_dtype != TPP_BF16 && cs_dtype != TPP_F32)
+    return set_error(TPP_E_UNSUPPORTED, "%s: cos/sin dtype", name);
+  if (ctx < Lmax || ctx > 0x7fffffff)
+    return set_error(TPP_E_INVALID, "%s: cos/sin hold %lld positions, fewer than the cache length %lld",
+                     name, (long long)ctx, (long long)Lmax);
+  if (Lmax < 1 || Lmax > 0x7fffffff) return set_error(TPP_E_INVALID, "%s: cache length", name);
+  const int64_t qs[3] = {0, 0, 0};
+  AttnArgs a = make_args(qkv, k_cache, v_cache, o, qs, k_strides, v_strides, os, B, 1, Lmax, Hq,
+                         Hkv, D, softmax_scale, window_left < 0 ? -1 : window_left, 0);
+  if (int rc = check_attn(name, a, D)) return rc;
+  if (!strides16(a)) return set_error(TPP_E_INVALID, "%s: 16-byte alignment required", name);
+  const OprojPlan pl = plan_oproj(B, Hq, D, Lmax, E);
+  DecodeFuse fz{qkv, q_norm_w, k_norm_w, cos, sin, cs_dtype, (int)ctx, eps};
+  char *ws = (char *)workspace;
+  DecodeOproj op{w_o, residual, (int *)(ws + kDecOpCtrOffset), (float *)(ws + pl.part_off), (int)E};
+  float *ws_o = (float *)(ws + kDecCounterBytes);
+  const dim3 grid(kOpXcds * kOpPerXcd), block(64 * kDecBigNW);
+  return TPP_DISPATCH_HALF(dtype, [&] {
+    if (Hq == 16)
+      attn_decode_kernel<T, 128, 2, kDecBigNW, true><<<grid, block, 0, st>>>(
+          a, seqlens, (int)Lmax, ws_o, nullptr, pl.chunk, pl.nsplit, fz, (int *)ws, op);
+    else
+      attn_decode_kernel<T, 128, 1, kDecBigNW, true><<<grid, block, 0, st>>>(
+          a, seqlens, (int)Lmax, ws_o, nullptr, pl.chunk, pl.nsplit, fz, (int *)ws, op);
+    return check_launch(name);
+  });
+}
+
+extern "C" int tpp_attn_decode_oproj_sync_errors(void *workspace, int *out, void *stream) {
+  const char *name = "tpp_attn_decode_oproj_sync_errors";
+  if (!workspace || !out) return set_error(TPP_E_INVALID, "%s: null pointer", name);
+  hipStream_t st = as_stream(stream);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return set_error(TPP_E_INVALID, "%s: not callable while the stream is being captured", name);
+  }
+  char *ctr = (char *)workspace + kDecOpCtrOffset;
+  int flag = 0;
+  if (hipMemcpyAsync(&flag, ctr + kOpErr * sizeof(int), sizeof(int), hipMemcpyDeviceToHost, st) !=
+          hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(TPP_E_LAUNCH, "%s: copy failed", name);
+  }
+  // a launch that gave up leaves the counters in an unknown state: zero them
+  if (flag && (hipMemsetAsync(ctr, 0, (kOpErr + 32) * sizeof(int), st) != hipSuccess ||
+               hipStreamSynchronize(st) != hipSuccess)) {
+    (void)hipGetLastError();
+    return set_error(TPP_E_LAUNCH, "%s: clearing the counters failed", name);
+  }
+  *out = flag;
+  return TPP_OK;
 }

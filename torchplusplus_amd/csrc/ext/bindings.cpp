@@ -722,9 +722,94 @@ at::Tensor attn_decode_fused(at::Tensor qkv, c10::optional<at::Tensor> q_norm_w,
   return o;
 }
 
+// decode attention with the fused prologue, then the output projection and
+// residual add (in place on `residual`); returns the attention output
+at::Tensor attn_decode_oproj(at::Tensor qkv, c10::optional<at::Tensor> q_norm_w,
+                             c10::optional<at::Tensor> k_norm_w, at::Tensor cos, at::Tensor sin,
+                             double eps, at::Tensor k_cache, at::Tensor v_cache,
+                             at::Tensor seqlens, at::Tensor w_o, at::Tensor residual,
+                             double softmax_scale, int64_t window_left) {
+  TORCH_CHECK(qkv.is_cuda() && qkv.is_contiguous() && is_half_or_bf16(qkv),
+              "qkv must be a contiguous CUDA half/bfloat16 tensor [B, 1, (Hq+2Hkv)*D]");
+  TORCH_CHECK(k_cache.is_cuda() && v_cache.is_cuda() && k_cache.dim() == 4 &&
+                  k_cache.sizes() == v_cache.sizes() && k_cache.stride(3) == 1 &&
+                  v_cache.stride(3) == 1 && k_cache.scalar_type() == qkv.scalar_type() &&
+                  v_cache.scalar_type() == qkv.scalar_type(),
+              "caches must be CUDA [B, Hkv, Lmax, D] of the qkv dtype");
+  const int64_t B = k_cache.size(0), Hkv = k_cache.size(1), Lmax = k_cache.size(2),
+                D = k_cache.size(3);
+  TORCH_CHECK(qkv.numel() % (B * D) == 0, "qkv size mismatch");
+  const int64_t Hq = qkv.numel() / (B * D) - 2 * Hkv;
+  TORCH_CHECK(Hq > 0 && Hq % Hkv == 0, "qkv size does not give a valid head count");
+  TORCH_CHECK(seqlens.is_cuda() && seqlens.scalar_type() == at::kInt && seqlens.numel() == B &&
+                  seqlens.is_contiguous(),
+              "seqlens must be a contiguous CUDA int32 tensor [B]");
+  TORCH_CHECK(cos.is_contiguous() && sin.is_contiguous() && cos.dim() == 2 && cos.size(1) == D &&
+                  sin.sizes() == cos.sizes() && sin.scalar_type() == cos.scalar_type() &&
+                  dtype_code(cos) >= 0,
+              "cos/sin must be contiguous [ctx, D] tables");
+  TORCH_CHECK(cos.size(0) >= Lmax, "cos/sin hold ", cos.size(0),
+              " positions, fewer than the cache length ", Lmax);
+  TORCH_CHECK(w_o.is_cuda() && w_o.dim() == 2 && w_o.size(1) == Hq * D && w_o.is_contiguous() &&
+                  w_o.scalar_type() == qkv.scalar_type(),
+              "w_o must be a contiguous [E, Hq*D] weight of the qkv dtype");
+  const int64_t E = w_o.size(0);
+  TORCH_CHECK(residual.is_cuda() && residual.is_contiguous() && residual.numel() == B * E &&
+                  residual.scalar_type() == qkv.scalar_type(),
+              "residual must be a contiguous [B, E] tensor of the qkv dtype");
+  const void *qw = norm_ptr(q_norm_w, qkv, D), *kw = norm_ptr(k_norm_w, qkv, D);
+  c10::DeviceGuard g(qkv.device());
+  auto o = torch::empty({B, 1, Hq, D}, qkv.options());
+  const size_t wsb = tpp_attn_decode_oproj_workspace_size(B, Hq, Hkv, D, Lmax, E);
+  at::Tensor ws = cached_workspace(qkv, wsb, 1);
+  const int64_t ks[3] = {k_cache.stride(0), k_cache.stride(2), k_cache.stride(1)};
+  const int64_t vs[3] = {v_cache.stride(0), v_cache.stride(2), v_cache.stride(1)};
+  check_rc(tpp_attn_decode_oproj(qkv.data_ptr(), qw, kw, cos.data_ptr(), sin.data_ptr(),
+                                 cos.size(0), dtype_code(cos), (float)eps, k_cache.data_ptr(),
+                                 v_cache.data_ptr(), o.data_ptr(), ks, vs,
+                                 seqlens.data_ptr<int32_t>(), w_o.data_ptr(), residual.data_ptr(),
+                                 B, Hq, Hkv, D, Lmax, E, (float)softmax_scale, (int)window_left,
+                                 dtype_code(qkv), ws.data_ptr(), (size_t)ws.numel() * 4,
+                                 cur_stream(qkv)),
+           "attn_decode_oproj");
+  return o;
+}
+
+// nonzero if a one-launch attn_decode_oproj on this device gave up waiting for
+// its workgroups since the last check; reads and clears the flag of every
+// decode-attention workspace of the device (as ffn_decode_sync_errors)
+int64_t attn_decode_sync_errors(at::Tensor like) {
+  TORCH_CHECK(like.is_cuda(), "attn_decode_sync_errors: expected a CUDA tensor");
+  c10::DeviceGuard g(like.device());
+  ScratchSlot &e = scratch_slot(like.device().index(), 1);
+  if (!e.t.defined()) return 0;
+  cached_workspace(like, 1, 1);
+  int64_t any = 0;
+  auto check = [&](at::Tensor &t) {
+    int out = 0;
+    check_rc(tpp_attn_decode_oproj_sync_errors(t.data_ptr(), &out, cur_stream(like)),
+             "attn_decode_sync_errors");
+    any |= out;
+  };
+  check(e.t);
+  for (auto &t : e.retired) check(t);
+  return any;
+}
+
 } // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("attn_decode_oproj", &attn_decode_oproj,
+        "decode attention (fused QK-norm + RoPE + KV append) then the output projection and the "
+        "residual add, in place on residual; returns the attention output",
+        py::arg("qkv"), py::arg("q_norm_w"), py::arg("k_norm_w"), py::arg("cos"), py::arg("sin"),
+        py::arg("eps"), py::arg("k_cache"), py::arg("v_cache"), py::arg("seqlens"),
+        py::arg("w_o"), py::arg("residual"), py::arg("softmax_scale") = 0.0,
+        py::arg("window_left") = -1);
+  m.def("attn_decode_sync_errors", &attn_decode_sync_errors,
+        "nonzero if a one-launch attn_decode_oproj gave up waiting for its workgroups since the "
+        "last check (its residual update was wrong); clears the flag",
+        py::arg("like"));
   m.def("attn_decode_fused", &attn_decode_fused,
         "decode attention with QK-norm + RoPE + KV append of the new token fused in",
         py::arg("qkv"), py::arg("q_norm_w"), py::arg("k_norm_w"), py::arg("cos"), py::arg("sin"),

@@ -11,11 +11,11 @@ Execution:
   * forward_impl keeps the residual stream in one buffer. For prefill it
     fuses each residual add into the next RMSNorm; for <= 16 tokens
     (decode) each RMSNorm is fused into the GEMV that reads it, each
-    residual add into the GEMV that writes it, the QK-norm + RoPE +
-    KV-append of the new token into the decode attention kernel, and the
-    whole FFN half (RMSNorm, SwiGLU gate/up, down, residual add) into one
-    launch, so a layer is 4 kernels: QKV GEMV, split-KV attention, o_proj
-    GEMV, FFN.
+    residual add into the kernel that writes it, the QK-norm + RoPE +
+    KV-append of the new token, the output projection and its residual add
+    into the decode attention kernel, and the whole FFN half (RMSNorm,
+    SwiGLU gate/up, down, residual add) into one launch, so a layer is 3
+    kernels: QKV GEMV, split-KV attention + o_proj, FFN.
   * GreedyDecoder captures one whole decode step (28 layers, lm_head,
     argmax, position advance) into a HIP graph and replays it per token, so
     the token loop issues one launch per token and never synchronises.
@@ -43,16 +43,19 @@ from torchplusplus_amd.llmops.llm import LLMInference
 _C = _ext()
 
 
-def check_ffn_decode(like: torch.Tensor) -> None:
-    """Raise if a one-launch decode FFN on `like`'s device gave up waiting for
-    its workgroups since the last check (it needs all 256 resident at once;
-    its output is then wrong). Clears the flag and the workspace counters.
+def check_decode_errors(like: torch.Tensor) -> None:
+    """Raise if a one-launch decode kernel on `like`'s device (the decode FFN,
+    the decode attention with the output projection) gave up waiting for its
+    workgroups since the last check (they need all 256 resident at once; the
+    output is then wrong). Clears the flags and the workspace counters.
     Synchronises the current stream."""
-    if _C.ffn_decode_sync_errors(like):
+    bad = [n for n, f in (("ffn_decode", _C.ffn_decode_sync_errors),
+                          ("attn_decode_oproj", _C.attn_decode_sync_errors)) if f(like)]
+    if bad:
         raise RuntimeError(
-            "ffn_decode: a one-launch decode FFN gave up waiting for its 256 workgroups (not all "
-            "were resident at once, e.g. other work held CUs), so tokens decoded since the last "
-            "check are wrong; the workspace was reset, decode again")
+            f"{', '.join(bad)}: a one-launch decode kernel gave up waiting for its 256 workgroups "
+            "(not all were resident at once, e.g. other work held CUs), so tokens decoded since "
+            "the last check are wrong; the workspaces were reset, decode again")
 
 
 @dataclass
@@ -154,7 +157,7 @@ class FastQwen3(LLMInference):
 
     def check_device_errors(self):
         if self.out_head.weight.is_cuda:
-            check_ffn_decode(self.out_head.weight)
+            check_decode_errors(self.out_head.weight)
 
     def get_num_layers(self) -> int:
         return self.cfg.n_layers
@@ -193,8 +196,11 @@ class FastQwen3(LLMInference):
             at, n1, n2 = blk.attn, blk.rms_norm1, blk.rms_norm2
             kv = kv_caches[i] if kv_caches is not None else None
             qkv = _C.gemv_fused(resid, at.fused_qkv_weight(), n1.weight, n1.eps)
-            o = at.attend(qkv, self.cos, self.sin, kv, cache_position)
-            _C.gemv_fused(o, at.out_projection.weight, None, 1e-6, resid)
+            if kv is not None and resid.shape[1] == 1:
+                at.attend_oproj(qkv, self.cos, self.sin, kv, cache_position, resid)
+            else:
+                o = at.attend(qkv, self.cos, self.sin, kv, cache_position)
+                _C.gemv_fused(o, at.out_projection.weight, None, 1e-6, resid)
             _C.ffn_decode(resid, n2.weight, n2.eps, blk.ffn.w_gu(), blk.ffn.linear_layer2.weight)
         return _C.gemv_fused(resid, self.out_head.weight, self.final_rmsnorm.weight,
                              self.final_rmsnorm.eps)
@@ -240,8 +246,7 @@ class GreedyDecoder:
             at, n1, n2 = blk.attn, blk.rms_norm1, blk.rms_norm2
             kc, vc = self.caches[i].k_cache[:B], self.caches[i].v_cache[:B]
             qkv = _C.gemv_fused(resid, at.fused_qkv_weight(), n1.weight, n1.eps)
-            o = at.decode_fused(qkv, m.cos, m.sin, kc, vc, self.seqlens)
-            _C.gemv_fused(o.view(B, 1, at.d_out), at.out_projection.weight, None, 1e-6, resid)
+            at.decode_oproj(qkv, m.cos, m.sin, kc, vc, self.seqlens, resid)
             _C.ffn_decode(resid, n2.weight, n2.eps, blk.ffn.w_gu(), blk.ffn.linear_layer2.weight)
         fn = m.final_rmsnorm
         _C.greedy_step(resid, m.out_head.weight, fn.weight, fn.eps, m.tok_embed.weight,
@@ -295,5 +300,5 @@ class GreedyDecoder:
         for c in self.caches:
             c.cache_len = position + n_steps
         if n_steps > 0:
-            check_ffn_decode(self.ids)
+            check_decode_errors(self.ids)
         return out
