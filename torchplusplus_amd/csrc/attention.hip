@@ -740,7 +740,7 @@ __device__ __forceinline__ f32x4 mfma16x32(typename VecT<T>::v8 a, typename VecT
 //  4. An agent-scope counter per column chunk finds the chunk's last XCD,
 //     which sums the 8 partials in XCD order (fixed: bit-reproducible) and
 //     updates the residual: T(residual + T(sum)).
-template <typename T, int D, int G, int NW>
+template <typename T, int D, int G, int NW, int MG>
 __device__ __forceinline__ void attn_decode_oproj_tail(const AttnArgs &p, const float *__restrict__ ws_o,
                                                        int nsplit, const DecodeOproj &op,
                                                        const T *s_w, T *s_o, f32x4 (*s_red)[64]) {
@@ -788,29 +788,29 @@ __device__ __forceinline__ void attn_decode_oproj_tail(const AttnArgs &p, const 
   __syncthreads();
 
   // ---- 2. merge the splits: item = (batch row, head, 4 columns); rows past
-  // B are zero (MFMA padding). Each split slot is D outputs, m, l, padding.
+  // B are zero (MFMA padding). Each split slot is D outputs, m, l, padding;
+  // the splits are read in groups of MG (nsplit = 32 / B is a multiple), all
+  // loads of a group before any use: one L2 round trip per group.
   for (int it = threadIdx.x; it < 16 * G * (D / 4); it += 64 * NW) {
     const int d4 = it % (D / 4), gi = (it / (D / 4)) % G, bb = it / (D / 4 * G);
     float r[4] = {0.f, 0.f, 0.f, 0.f};
     if (bb < B) {
       const float *sl = ws_o + ((int64_t)bb * p.Hq + x * G + gi) * nsplit * (D + 32);
-      constexpr int MG = 8;
       float mu = -INFINITY, ls = 0.f, os[4] = {0.f, 0.f, 0.f, 0.f};
       for (int s0 = 0; s0 < nsplit; s0 += MG) {
         float mv[MG], lv[MG];
         f32x4 ov[MG];
 #pragma unroll
         for (int jj = 0; jj < MG; ++jj) {
-          const int sp = s0 + jj < nsplit ? s0 + jj : nsplit - 1;
-          const float *q = sl + (int64_t)sp * (D + 32);
-          mv[jj] = q[D];
-          lv[jj] = q[D + 1];
+          const float *q = sl + (int64_t)(s0 + jj) * (D + 32);
+          const float2 ml = *reinterpret_cast<const float2 *>(q + D);
+          mv[jj] = ml.x;
+          lv[jj] = ml.y;
           ov[jj] = *reinterpret_cast<const f32x4 *>(q + 4 * d4);
         }
         float mx = mu;
 #pragma unroll
-        for (int jj = 0; jj < MG; ++jj)
-          if (s0 + jj < nsplit) mx = fmaxf(mx, mv[jj]);
+        for (int jj = 0; jj < MG; ++jj) mx = fmaxf(mx, mv[jj]);
         const float mn = mx == -INFINITY ? 0.f : mx;
         const float a = mu == -INFINITY ? 0.f : exp2f(mu - mn);
         ls *= a;
@@ -818,7 +818,7 @@ __device__ __forceinline__ void attn_decode_oproj_tail(const AttnArgs &p, const 
         for (int c = 0; c < 4; ++c) os[c] *= a;
 #pragma unroll
         for (int jj = 0; jj < MG; ++jj) {
-          const float wgt = s0 + jj < nsplit ? exp2f(mv[jj] - mn) : 0.f;
+          const float wgt = exp2f(mv[jj] - mn);
           ls += wgt * lv[jj];
 #pragma unroll
           for (int c = 0; c < 4; ++c) os[c] += wgt * ov[jj][c];
@@ -1233,7 +1233,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
     }
   }
   if constexpr (OP) {
-    attn_decode_oproj_tail<T, D, G, NW>(p, ws_o, nsplit, op, s_w, s_o, s_red);
+    // nsplit = 32 / B: 2, 4 or a multiple of 8
+    if (nsplit == 2) attn_decode_oproj_tail<T, D, G, NW, 2>(p, ws_o, nsplit, op, s_w, s_o, s_red);
+    else if (nsplit == 4) attn_decode_oproj_tail<T, D, G, NW, 4>(p, ws_o, nsplit, op, s_w, s_o, s_red);
+    else attn_decode_oproj_tail<T, D, G, NW, 8>(p, ws_o, nsplit, op, s_w, s_o, s_red);
     return;
   }
   if (!counters || nsplit == 1) return;
