@@ -77,6 +77,15 @@ def mfma_entry(name, us, flops):
             "TFLOP/s": round(tf, 1), "frac": round(tf / MFMA_PEAK_TFLOPS, 4)}
 
 
+def oproj_bytes(B, H, Hkv, D, E, L):
+    """Algorithmic HBM bytes of one decode attention + o_proj launch at cache
+    length L: the L-1 cached K/V rows of every (sequence, KV head), the new
+    token's qkv row, its K/V rows written to the cache, the projection weight,
+    the residual read and written, the attention output written."""
+    return (2 * B * Hkv * (L - 1) * D * 2 + B * (H + 2 * Hkv) * D * 2 + 2 * B * Hkv * D * 2
+            + E * H * D * 2 + 2 * B * E * 2 + B * H * D * 2)
+
+
 def measure_kernels(model, dec, cfg, L):
     """Per-kernel timings at the decode (cache length L) and prefill shapes.
     Each launch cycles over the 28 layers' weights / caches, so the bytes come
@@ -109,9 +118,24 @@ def measure_kernels(model, dec, cfg, L):
         C.attn_decode(q, c.k_cache, c.v_cache, seq, 0.0, -1, o)
 
     us = event_time_us(attn, nl)
-    attn_bytes = 2 * B * Hkv * L * D * 2 + 2 * B * H * D * 2
-    out.append(hbm_entry("attn_decode_kernel (splits merged in-kernel) B8 16/8 d128 L%d" % L, us, attn_bytes))
-    attn_us = us
+    out.append(hbm_entry("attn_decode_kernel (splits merged in-kernel) B8 16/8 d128 L%d" % L, us,
+                         2 * B * Hkv * L * D * 2 + 2 * B * H * D * 2))
+
+    # the decode step's attention launch: QK-norm + RoPE + K/V append of the
+    # new token, attention over L keys, output projection + residual add
+    qkv1 = (0.5 * torch.randn(B, 1, (H + 2 * Hkv) * D, generator=g, device=dev)).to(dt)
+    reso = torch.randn(B, 1, E, generator=g, device=dev).to(dt)
+
+    def attn_op():
+        i = cyc()
+        c, at = caches[i], blocks[i].attn
+        C.attn_decode_oproj(qkv1, at.q_norm.weight, at.k_norm.weight, model.cos, model.sin, 1e-6,
+                            c.k_cache, c.v_cache, seq, at.out_projection.weight, reso)
+
+    attn_us = event_time_us(attn_op, nl)
+    attn_bytes = oproj_bytes(B, H, Hkv, D, E, L)
+    out.append(hbm_entry("attn_decode_kernel<oproj> (attention + o_proj + residual, one launch) "
+                         "B8 16/8 d128 L%d, W_o [1024x2048]" % L, attn_us, attn_bytes))
 
     def gemv_entry(name, wget, n, k, xin, fn=None):
         def run():
@@ -125,8 +149,9 @@ def measure_kernels(model, dec, cfg, L):
                x1, lambda a, b: C.gemv_fused(a, b, nw, 1e-6))
     xo = torch.randn(B, 1, H * D, generator=g, device=dev).to(dt)
     res = torch.randn(B, 1, E, generator=g, device=dev).to(dt)
-    gemv_entry("gemv o_proj +residual [8x2048]x[1024x2048]^T", lambda b: b.attn.out_projection.weight,
-               E, H * D, xo, lambda a, b: C.gemv_fused(a, b, None, 1e-6, res))
+    gemv_entry("gemv o_proj +residual [8x2048]x[1024x2048]^T (two-launch path, not in the step)",
+               lambda b: b.attn.out_projection.weight, E, H * D, xo,
+               lambda a, b: C.gemv_fused(a, b, None, 1e-6, res))
     # the decode step's FFN half: RMSNorm + gate/up SwiGLU + down + residual in
     # one launch (weights of all 28 layers in turn, residual updated in place)
     resf = torch.randn(B, 1, E, generator=g, device=dev).to(dt)
@@ -450,7 +475,7 @@ def cpu_baseline(model, cfg, steps: int = 5, warmup: int = 2, full: bool = False
                       f"batch-{BATCH} prefill then {n_dec} greedy decode steps; oracle/qwen3.py"}
 
 
-TRAFFIC_GROUPS = ["attn", "gemv_qkv", "gemv_o", "gemv_gu", "gemv_down", "ffn", "lm_head", "rmsnorm",
+TRAFFIC_GROUPS = ["attn_oproj", "attn", "gemv_qkv", "gemv_o", "gemv_gu", "gemv_down", "ffn", "lm_head", "rmsnorm",
                   "layernorm", "rope", "hgemv_3072", "hgemv_1024", "copy"]
 
 
@@ -479,7 +504,18 @@ def traffic_probe(group: str, L: int, launches: int = 16):
         return lambda i: sets[i % n]
 
     launch, nbytes = None, 0
-    if group == "attn":
+    if group == "attn_oproj":
+        get = rot(8, lambda: (rn(B, Hkv, L, D), rn(B, Hkv, L, D), rn(E, H * D, std=0.02)))
+        qkv, seq = rn(B, 1, (H + 2 * Hkv) * D, std=0.5), torch.full((B,), L, dtype=torch.int32, device=dev)
+        res, nw = rn(B, 1, E), torch.ones(D, dtype=torch.bfloat16, device=dev)
+        from torchplusplus_amd.dlops.rope import compute_rope_params
+        cos, sin = compute_rope_params(D, 1e6, L + 1, device=dev)
+
+        def launch(i):
+            kc, vc, wo = get(i)
+            return C.attn_decode_oproj(qkv, nw, nw, cos, sin, 1e-6, kc, vc, seq, wo, res)
+        nbytes = oproj_bytes(B, H, Hkv, D, E, L)
+    elif group == "attn":
         get = rot(8, lambda: (rn(B, Hkv, L, D), rn(B, Hkv, L, D)))
         q, seq = rn(B, 1, H, D), torch.full((B,), L, dtype=torch.int32, device=dev)
         o = torch.empty_like(q)
@@ -549,7 +585,7 @@ def measured_traffic(cache_len: int):
     measured at this cache length; else None."""
     import glob
     import re
-    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "attn_decode_b8_l*_traffic.md"))):
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "attn_decode_oproj_b8_l*_traffic.md"))):
         txt = open(path).read()
         b = re.search(r"^traffic_bytes_per_launch: (\d+)$", txt, re.M)
         L = re.search(r"^traffic_cache_len: (\d+)$", txt, re.M)
@@ -700,7 +736,8 @@ def main():
                                "head_dim 128, SwiGLU 3072, vocab 151936), batch 8, prefill 2048",
                    "global_batch": BATCH, "prefill_len": PREFILL, "decode_steps": K,
                    "parallelism": "single GPU"},
-        "roofline": {"kernel": "attn_decode_kernel", "bound": "hbm",
+        "roofline": {"kernel": "attn_decode_kernel<oproj> (decode attention + o_proj + residual)",
+                     "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(L),
                      "bytes_per_launch": attn_bytes, "avg_launch_us": round(attn_us, 3),

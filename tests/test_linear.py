@@ -156,6 +156,27 @@ def test_gemv_parity(dev, dtype, bsz, n, k):
     close(y, oracle.gemv(x, w), what=f"gemv b{bsz} {n}x{k}")
 
 
+@pytest.mark.parametrize("n,k", [(257, 8), (100, 520), (2049, 4096), (3, 4088), (5000, 1536)])
+@pytest.mark.parametrize("epi", ["plain", "gelu", "residual"])
+def test_gemv_one_row_input(dev, n, k, epi):
+    """Batch 1 (the reference's hgemv): one weight row per wave, 1 to 8
+    16-byte chunks per lane, K not a multiple of 512 (the last chunks of a
+    row past K), more rows than waves of one block per CU; plain, bias + GeLU
+    and residual epilogues."""
+    x, w, b = _mk(1, n, k, torch.float16, seed=n + k)
+    xd, wd = x.to(dev), w.to(dev)
+    if epi == "plain":
+        close(ext().gemv(xd, wd), oracle.gemv(x, w), what=f"b1 {n}x{k}")
+    elif epi == "gelu":
+        close(ext().gemv(xd, wd, b.to(dev), ACTS["gelu"]), oracle.linear_act(x, w, b, "gelu"),
+              what=f"b1 gelu {n}x{k}")
+    else:
+        r = torch.randn(1, n, generator=torch.Generator().manual_seed(k)).half()
+        rd = r.to(dev)
+        ext().gemv_fused(xd, wd, None, 1e-6, rd)
+        close(rd, (r.float() + oracle.gemv(x, w).float()).half(), what=f"b1 residual {n}x{k}")
+
+
 def test_gemv_repeated_calls_are_deterministic(dev):
     """No cross-block reduction: repeated calls give bit-identical results."""
     x, w, _ = _mk(8, 1024, 3072, torch.bfloat16, seed=6)
