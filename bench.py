@@ -458,10 +458,13 @@ def cpu_baseline(model, cfg, steps: int = 5, warmup: int = 2, full: bool = False
         t0 = time.perf_counter()
         logits = orc.forward(ids, 0)
         t1 = time.perf_counter()
+        log(f"[bench] cpu full rep {r}: prefill {t1 - t0:.1f} s")
         nxt = logits[:, -1].argmax(-1, keepdim=True)
         for s in range(n_dec):
             logits = orc.forward(nxt, PREFILL + s)
             nxt = logits[:, -1].argmax(-1, keepdim=True)
+            if s % 8 == 7:
+                log(f"[bench] cpu full rep {r}: {s + 1} decode steps")
         t2 = time.perf_counter()
         log(f"[bench] cpu full rep {r}: prefill {t1 - t0:.1f} s, {n_dec} steps {t2 - t1:.1f} s")
         if r >= warmup:
