@@ -362,6 +362,13 @@ int tpp_attn_decode_oproj(const void *qkv, const void *q_norm_w,
  * rules as tpp_ffn_decode_sync_errors. */
 int tpp_attn_decode_oproj_sync_errors(void *workspace, int *out, void *stream);
 
+/* Test hook: marks a workspace as if a one-launch decode kernel had given up
+ * waiting (kernel 0: tpp_attn_decode_oproj, 1: tpp_ffn_decode): sets its flag
+ * and leaves a stray arrival count, by host copies; synchronises `stream`.
+ * For tests of the error path that must not make a kernel wait. No
+ * counterpart in the reference. */
+int tpp_decode_force_sync_error(void *workspace, int kernel, void *stream);
+
 /* ---- sampling ------------------------------------------------------------ */
 
 /* Greedy sampling: out[b] = argmax_n x[b, n] for x [B, ldx] (first index of

@@ -153,3 +153,27 @@ def test_graph_replay_after_decode_workspace_grew(dev):
     torch.cuda.synchronize()
     del junk
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("kernel", [0, 1], ids=["attn_decode_oproj", "ffn_decode"])
+@torch.inference_mode()
+def test_decode_sync_error_raises_then_recovers(dev, kernel):
+    """A one-launch decode kernel that gave up waiting (flag forced from the
+    host, no kernel made to wait) makes the next decode loop raise; the
+    check clears the flag and the counters, and the following loop gives the
+    tokens of an undisturbed run. Config-5 layer shapes (E 1024, 16/8 heads,
+    I 3072), 2 layers, so both one-launch kernels run."""
+    import torchplusplus_amd
+
+    info = torchplusplus_amd.prepare_device(dev)
+    if info["cu_count"] != 256 or not info["xcd_local"]:
+        pytest.skip("the one-launch decode kernels need 256 CUs and XCD placement")
+    cfg = QwenConfig(vocab_size=512, context_length=256, n_layers=2)
+    m = _model(dev, cfg, seed=13)
+    ids = torch.randint(0, cfg.vocab_size, (8, 20), generator=torch.Generator().manual_seed(14)).to(dev)
+    want = m.generate_greedy(ids, 5)
+    from torchplusplus_amd._native import ext
+    ext()._force_decode_sync_error(ids, kernel)
+    with pytest.raises(RuntimeError, match="gave up waiting"):
+        m.generate_greedy(ids, 5)
+    assert torch.equal(m.generate_greedy(ids, 5), want)

@@ -715,6 +715,9 @@ constexpr unsigned kOpSpinLimit = 1u << 20;
 // counter region (ints, each counter on its own 128-byte line) at
 // kDecOpCtrOffset of the workspace: arrive[8], depart[8], chunk[32], err
 constexpr int kOpArrive = 0, kOpDepart = 8 * 32, kOpChunk = 16 * 32, kOpErr = 48 * 32;
+static_assert(kAttnOprojCtrOffset == (size_t)kDecOpCtrOffset &&
+                  kAttnOprojErrOffset == (size_t)kDecOpCtrOffset + kOpErr * sizeof(int),
+              "counter and flag offsets shared with ffn.hip");
 
 template <typename T>
 __device__ __forceinline__ f32x4 mfma16x32(typename VecT<T>::v8 a, typename VecT<T>::v8 b, f32x4 c) {

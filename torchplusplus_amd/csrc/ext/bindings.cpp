@@ -537,6 +537,18 @@ int64_t ffn_decode_sync_errors(at::Tensor like) {
   return any;
 }
 
+// test hook: mark the device's current decode-attention (kernel 0) or decode
+// FFN (kernel 1) workspace as if a one-launch kernel had given up waiting
+void force_decode_sync_error(at::Tensor like, int64_t kernel) {
+  TORCH_CHECK(like.is_cuda() && (kernel == 0 || kernel == 1), "force_decode_sync_error: bad arguments");
+  c10::DeviceGuard g(like.device());
+  ScratchSlot &e = scratch_slot(like.device().index(), kernel == 0 ? 1 : 2);
+  TORCH_CHECK(e.t.defined(), "force_decode_sync_error: no workspace yet");
+  cached_workspace(like, 1, kernel == 0 ? 1 : 2);
+  check_rc(tpp_decode_force_sync_error(e.t.data_ptr(), (int)kernel, cur_stream(like)),
+           "force_decode_sync_error");
+}
+
 // One-time device checks of the XCD-local kernels, outside capture
 // (tpp_prepare_device): returns (workgroups with equal id % 8 share an XCD,
 // CU count).
@@ -823,6 +835,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "nonzero if a one-launch decode FFN gave up waiting for its workgroups since the last "
         "check (its output was wrong); clears the flag",
         py::arg("like"));
+  m.def("_force_decode_sync_error", &force_decode_sync_error,
+        "test hook: flag the device's decode-attention (0) or decode-FFN (1) workspace as if a "
+        "one-launch kernel had given up waiting", py::arg("like"), py::arg("kernel"));
   m.def("prepare_device", &prepare_device,
         "one-time XCD placement probe and CU count of the tensor's device (outside capture)",
         py::arg("like"));

@@ -449,3 +449,24 @@ extern "C" int tpp_ffn_decode_sync_errors(void *workspace, int *out, void *strea
   *out = flag;
   return TPP_OK;
 }
+
+extern "C" int tpp_decode_force_sync_error(void *workspace, int kernel, void *stream) {
+  const char *name = "tpp_decode_force_sync_error";
+  if (!workspace || (kernel != 0 && kernel != 1))
+    return set_error(TPP_E_INVALID, "%s: null workspace or unknown kernel %d", name, kernel);
+  // kernel 0: tpp_attn_decode_oproj's flag, 1: tpp_ffn_decode's; a stray
+  // arrival count is left as well, as a launch that gave up would
+  static const int kOne[2] = {1, 5};
+  const size_t err_off = kernel == 0 ? kAttnOprojErrOffset : kFfnOffErr;
+  const size_t ctr_off = kernel == 0 ? kAttnOprojCtrOffset : kFfnOffArrive;
+  hipStream_t st = as_stream(stream);
+  if (hipMemcpyAsync((char *)workspace + err_off, &kOne[0], sizeof(int), hipMemcpyHostToDevice, st) !=
+          hipSuccess ||
+      hipMemcpyAsync((char *)workspace + ctr_off, &kOne[1], sizeof(int), hipMemcpyHostToDevice, st) !=
+          hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(TPP_E_LAUNCH, "%s: copy failed", name);
+  }
+  return TPP_OK;
+}

@@ -299,6 +299,11 @@ template <int N, typename F> __device__ __forceinline__ void static_for(F &&f) {
 } // namespace tpp
 
 // Dispatch a body over fp16/bf16. `T` names the element type inside.
+// byte offsets in a tpp_attn_decode_oproj workspace: the folded projection's
+// counter region and its give-up flag (attention.hip lays them out)
+constexpr size_t kAttnOprojCtrOffset = 32768;
+constexpr size_t kAttnOprojErrOffset = kAttnOprojCtrOffset + 48 * 32 * sizeof(int);
+
 #define TPP_DISPATCH_HALF(dtype, ...)                                        \
   [&]() -> int {                                                             \
     if ((dtype) == TPP_F16) {                                                \
