@@ -100,3 +100,27 @@ def test_config5_against_oracle(dev, model):
         got = model.forward(step.to(dev), use_cache=True, cache_position=S + t)
         _check(got, orc16.forward(step, S + t), orc32.forward(step, S + t),
                f"config 5 decode step {t}")
+
+
+@torch.inference_mode()
+def test_config5_batch8_against_oracle(dev, model):
+    """The benchmark's batch (8 sequences) through all 28 layers against the
+    CPU oracle: last-position prefill logits of a 256-token prefix and 2
+    teacher-forced decode steps, which run the decode kernels the benchmark
+    times (the folded attention + output projection with 4 splits per
+    sequence, the one-launch FFN) on every sequence; same two-sided check."""
+    B, S = 8, 256
+    ids = torch.randint(0, CFG.vocab_size, (B, S + 2), generator=torch.Generator().manual_seed(3))
+    model.setup_kv_cache(S + 2, B)
+    model.reset_kv_cache()
+    orc16 = Qwen3Oracle(model.state_dict(), CFG, ROPE_CTX)
+    orc32 = Qwen3Oracle({}, QwenConfig(dtype=torch.float32), ROPE_CTX)
+    orc32.w = orc16.w
+    got = model.forward(ids[:, :S].to(dev), use_cache=True, cache_position=0)
+    _check(got[:, -1], orc16.forward(ids[:, :S], 0)[:, -1], orc32.forward(ids[:, :S], 0)[:, -1],
+           "config 5 batch 8 prefill, last position")
+    for t in range(2):
+        step = ids[:, S + t:S + t + 1]
+        got = model.forward(step.to(dev), use_cache=True, cache_position=S + t)
+        _check(got, orc16.forward(step, S + t), orc32.forward(step, S + t),
+               f"config 5 batch 8 decode step {t}")
