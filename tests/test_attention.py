@@ -282,16 +282,16 @@ def test_decode_fused_model_shape_split_merge(dev, lens):
     assert torch.equal(got, got2), "repeated call differs"
 
 
-def _oproj_inputs(B, hq, hkv, Lmax, lens, seed, E=1024, D=128):
+def _oproj_inputs(B, hq, hkv, Lmax, lens, seed, E=1024, D=128, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
-    qkv = torch.randn(B, 1, (hq + 2 * hkv) * D, generator=g).bfloat16()
-    qw = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
-    kw = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    qkv = torch.randn(B, 1, (hq + 2 * hkv) * D, generator=g).to(dtype)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype)
     cos, sin = oracle.compute_rope_params(D, 1e6, Lmax + 1)
-    kc = torch.randn(B, hkv, Lmax, D, generator=g).bfloat16()
-    vc = torch.randn(B, hkv, Lmax, D, generator=g).bfloat16()
-    w_o = (0.02 * torch.randn(E, hq * D, generator=g)).bfloat16()
-    resid = torch.randn(B, 1, E, generator=g).bfloat16()
+    kc = torch.randn(B, hkv, Lmax, D, generator=g).to(dtype)
+    vc = torch.randn(B, hkv, Lmax, D, generator=g).to(dtype)
+    w_o = (0.02 * torch.randn(E, hq * D, generator=g)).to(dtype)
+    resid = torch.randn(B, 1, E, generator=g).to(dtype)
     return qkv, qw, kw, cos, sin, kc, vc, w_o, resid, torch.tensor(lens, dtype=torch.int32)
 
 
@@ -377,15 +377,20 @@ def test_decode_oproj_model_shape(dev, lens):
     assert int(ws[:65536].view(torch.int32).abs().sum()) == 0, "counters not back at zero"
 
 
-@pytest.mark.parametrize("B,hq", [(1, 16), (2, 16), (4, 16), (16, 16), (8, 8), (16, 8)])
-def test_decode_oproj_batches_and_groups(dev, B, hq):
+@pytest.mark.parametrize("B,hq,dtype", [(1, 16, torch.bfloat16), (2, 16, torch.bfloat16),
+                                        (4, 16, torch.bfloat16), (16, 16, torch.bfloat16),
+                                        (8, 8, torch.bfloat16), (16, 8, torch.bfloat16),
+                                        (8, 16, torch.float16), (1, 8, torch.float16)])
+def test_decode_oproj_batches_and_groups(dev, B, hq, dtype):
     """The one-launch path at every batch it takes (32 / B splits per
-    sequence; B = 1 leaves most splits without a key) and with one query head
-    per KV head (G = 1, K slice 128), ragged lengths, vs the oracle."""
+    sequence; B = 1 leaves most splits without a key), with one query head
+    per KV head (G = 1, K slice 128), ragged lengths, bf16 and fp16 (the
+    reference's model dtype), vs the oracle."""
     hkv, Lmax = 8, 700
     g = torch.Generator().manual_seed(B * 31 + hq)
     lens = torch.randint(1, Lmax + 1, (B,), generator=g).tolist()
-    qkv, qw, kw, cos, sin, kc, vc, w_o, resid, seqlens = _oproj_inputs(B, hq, hkv, Lmax, lens, 23 + B)
+    qkv, qw, kw, cos, sin, kc, vc, w_o, resid, seqlens = _oproj_inputs(B, hq, hkv, Lmax, lens, 23 + B,
+                                                                       dtype=dtype)
     e_o, e_res, _, _ = _oproj_oracle(qkv, qw, kw, cos, sin, kc, vc, w_o, resid, seqlens, hq, hkv)
     from torchplusplus_amd._native import ext
 
@@ -393,8 +398,8 @@ def test_decode_oproj_batches_and_groups(dev, B, hq):
     rd = resid.to(dev)
     o = C.attn_decode_oproj(qkv.to(dev), qw.to(dev), kw.to(dev), cos.to(dev), sin.to(dev), 1e-6,
                             kc.to(dev), vc.to(dev), seqlens.to(dev), w_o.to(dev), rd)
-    close(o, e_o, what=f"oproj decode B={B} Hq={hq}: attention output")
-    close(rd, e_res, what=f"oproj decode B={B} Hq={hq}: residual")
+    close(o, e_o, what=f"oproj decode B={B} Hq={hq} {dtype}: attention output")
+    close(rd, e_res, what=f"oproj decode B={B} Hq={hq} {dtype}: residual")
 
 
 def test_decode_oproj_unfolded_shape(dev):
