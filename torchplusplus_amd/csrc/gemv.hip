@@ -793,40 +793,54 @@ static bool launch_wide(const GemvArgs &a, hipStream_t st) {
 // One input row (the reference's hgemv, y = A x, hgemv_kernels.cuh:19-85):
 // a wave owns one weight row and reads it whole, lane l taking the 16-byte
 // chunks l, l + 64, ... (CPL per lane), so each instruction reads a
-// contiguous 1 KB of the row. Every weight and input load is issued before
-// the first product (chunks past the row end read chunk 0 and are multiplied
-// by 0), then fp32 products, a DPP wave reduction and the epilogue in one
-// lane: no LDS, no barrier, no MFMA padding, one block per CU. (Measured on
-// [1x3072]x[1024x3072]^T: a row per wave 3.06 us, two or four rows per wave
-// 3.7 / 4.5 us, a row split over two waves with an LDS sum 3.14 us.)
+// contiguous 1 KB of the row. The input row goes to LDS once per workgroup
+// by LDS-DMA (its CPL instructions dealt to the waves), ahead of every
+// weight load; chunks past the row end read chunk 0 and are multiplied by
+// 0. Then fp32 products, a DPP wave reduction and the epilogue in one lane:
+// no MFMA padding, one block per CU. (Measured on [1x3072]x[1024x3072]^T: a
+// row per wave 3.06 us, two or four rows per wave 3.7 / 4.5 us, a row split
+// over two waves with an LDS sum 3.14 us; the input through LDS instead of
+// read by every wave (6 MB of L2 reads per launch for 6 MB of weights),
+// 3.13-3.17 against 3.20-3.21 us in paired runs, the [1x1024] shape equal.)
 constexpr int kB1MaxLoads = 8; // 16-byte weight loads per lane
 
 template <typename T, int EPI, int ACT, int CPL>
 __global__ __launch_bounds__(1024) void gemv_b1_kernel(GemvArgs a) {
   typedef typename VecT<T>::v8 V8;
+  __shared__ __attribute__((aligned(16))) V8 s_x[CPL * 64];
   const int lane = lane_id();
-  const int64_t n = (int64_t)blockIdx.x * (blockDim.x / kWave) + wave_id();
-  if (n >= a.N) return; // whole waves; no barrier below
+  const int w = __builtin_amdgcn_readfirstlane(wave_id()), nwv = blockDim.x / kWave;
+  const int64_t n = (int64_t)blockIdx.x * nwv + w;
+  const bool live = n < a.N; // waves past N still take part in the barrier
   const int nch = (int)(a.K / 8);
   const T *x = (const T *)a.x;
-  const T *W = (const T *)a.W + n * a.K;
-  V8 xv[CPL], wr[CPL];
+  const T *W = (const T *)a.W + (live ? n : 0) * a.K;
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
+    if (i % nwv != w) continue; // wave-uniform
     const int c = lane + 64 * i;
-    xv[i] = *reinterpret_cast<const V8 *>(x + (int64_t)(c < nch ? c : 0) * 8);
+    __builtin_amdgcn_global_load_lds((const void *)(x + (int64_t)(c < nch ? c : 0) * 8),
+                                     (__attribute__((address_space(3))) void *)(s_x + i * 64),
+                                     16, 0, 0);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  V8 wr[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = lane + 64 * i;
     wr[i] = ld_nt(reinterpret_cast<const V8 *>(W + (int64_t)(c < nch ? c : 0) * 8));
   }
+  __builtin_amdgcn_sched_barrier(0);
+  vm_wait<CPL>(); // this wave's input DMA (issued before its CPL weight loads)
+  lds_barrier();  // every wave's
+  if (!live) return;
   float acc = 0.f;
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
+    const V8 xv = s_x[i * 64 + lane];
     const float on = lane + 64 * i < nch ? 1.f : 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += (on * to_f32(xv[i][e])) * to_f32(wr[i][e]);
+    for (int e = 0; e < 8; ++e) acc += (on * to_f32(xv[e])) * to_f32(wr[i][e]);
   }
   acc = wave_sum(acc);
   if (lane == 0) {
