@@ -648,6 +648,11 @@ def kernel_probe(name: str, reps: int = 5):
 CPU_MALLOC_TUNABLES = "glibc.malloc.mmap_threshold=4294967295:glibc.malloc.trim_threshold=4294967295"
 
 
+def _under_profiler() -> bool:
+    """rocprofv3 runs the program with its tool library preloaded."""
+    return "rocprof" in os.environ.get("LD_PRELOAD", "") or any(k.startswith("ROCPROF") for k in os.environ)
+
+
 def start_cpu_child(args):
     """The CPU baseline runs in a child process with the malloc settings
     above (they are read at process start). It is started before this
@@ -730,9 +735,17 @@ def main():
             traffic_probe(args.traffic_probe, PREFILL + args.steps // 2)
         return
 
+    # the CPU-baseline process is started first, before this one loads the HIP
+    # library; not under a profiler, whose preloaded library may have set up
+    # the GPU in this process already
+    child = None
+    if not args.no_cpu_baseline:
+        if _under_profiler():
+            log("[bench] profiler detected: no CPU baseline in this run")
+        else:
+            child = start_cpu_child(args)
     from torchplusplus_amd.fastqwen3 import FastQwen3, GreedyDecoder, QwenConfig
 
-    child = None if args.no_cpu_baseline else start_cpu_child(args)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     cfg = QwenConfig(dtype=torch.bfloat16)
