@@ -667,12 +667,21 @@ def start_cpu_child(args):
     return subprocess.Popen(cmd, env=env, stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True)
 
 
-def finish_cpu_child(child) -> dict:
-    """Signal the child, wait for its JSON line (its progress goes to stderr)."""
-    out, _ = child.communicate("go\n")
+def finish_cpu_child(child, timeout_s: float):
+    """Signal the child, wait for its JSON line (its progress goes to
+    stderr). A failed or overrunning child costs the line its CPU figures
+    only: None, with the reason logged."""
+    try:
+        out, _ = child.communicate("go\n", timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        child.kill()
+        child.communicate()
+        log(f"[bench] cpu baseline: no result within {timeout_s:.0f} s, left out")
+        return None
     lines = [ln for ln in out.splitlines() if ln.startswith("{")]
     if child.returncode != 0 or not lines:
-        raise RuntimeError(f"CPU baseline process failed (exit {child.returncode})")
+        log(f"[bench] cpu baseline process failed (exit {child.returncode}), left out")
+        return None
     return json.loads(lines[-1])
 
 
@@ -796,10 +805,11 @@ def main():
     cpu = None
     if child is not None:
         log("[bench] cpu baseline ...")
-        res = finish_cpu_child(child)
-        cpu = res["cpu_baseline"]
-        apply_cpu_configs(configs, res["cpu_configs"])
-        log("[bench] cpu baseline and config timings done")
+        res = finish_cpu_child(child, 3600.0 if args.cpu_full else 900.0)
+        if res is not None:
+            cpu = res["cpu_baseline"]
+            apply_cpu_configs(configs, res["cpu_configs"])
+            log("[bench] cpu baseline and config timings done")
 
     achieved = attn_bytes / attn_us / 1e3
     line = {
