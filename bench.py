@@ -187,8 +187,23 @@ def measure_kernels(model, dec, cfg, L):
                          2 * M * (H + 2 * Hkv) * D * 2 + 2 * PREFILL * D * 2))
     del qkv, qo
     xp = torch.randn(M, E, generator=g, device=dev).to(dt)
-    t = event_time_us(lambda: C.linear(xp, blocks[cyc()].attn.fused_qkv_weight(), None, 0), nl)
-    out.append(mfma_entry("gemm qkv [16384x1024]x[4096x1024]^T", t, 2 * M * 4096 * E))
+    # plain prefill projections: as dispatched (hipBLASLt from one 256x256
+    # tile per CU up) and on the hand-written MFMA kernel (dispatch off)
+    from torchplusplus_amd._native import lib
+    xo_p = torch.randn(M, H * D, generator=g, device=dev).to(dt)
+    xd_p = torch.randn(M, I, generator=g, device=dev).to(dt)
+    plain = (("gemm qkv [16384x1024]x[4096x1024]^T", xp, lambda b: b.attn.fused_qkv_weight(), 4096, E),
+             ("gemm o_proj [16384x2048]x[1024x2048]^T", xo_p, lambda b: b.attn.out_projection.weight, E, H * D),
+             ("gemm down [16384x3072]x[1024x3072]^T", xd_p, lambda b: b.ffn.linear_layer2.weight, E, I))
+    for vendor, tag in ((1, "hipBLASLt (dispatched)"), (0, "MFMA kernel")):
+        prev = lib().tpp_gemm_vendor(vendor)
+        try:
+            for name, xin, wget, n, k in plain:
+                t = event_time_us(lambda: C.linear(xin, wget(blocks[cyc()]), None, 0), nl)
+                out.append(mfma_entry(f"{name}, {tag}", t, 2 * M * n * k))
+        finally:
+            lib().tpp_gemm_vendor(prev)
+    del xo_p, xd_p
     t = event_time_us(lambda: C.linear_swiglu(xp, blocks[cyc()].ffn.w_gu()), nl)
     out.append(mfma_entry("gemm swiglu [16384x1024]x[6144x1024]^T", t, 2 * M * 2 * I * E))
     qp = torch.randn(BATCH, PREFILL, H, D, generator=g, device=dev).to(dt)

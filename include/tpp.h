@@ -7,6 +7,8 @@
  *  - All tensor arguments are caller-owned DEVICE pointers. No entry point
  *    allocates device memory; ops that need scratch take a `workspace`
  *    pointer whose size is returned by the matching *_workspace_size call.
+ *    (The first large plain GEMM on a device creates a hipBLASLt handle,
+ *    which loads that library's kernels; its GEMMs use no workspace.)
  *  - `stream` is a hipStream_t passed as void* (NULL = the legacy default
  *    stream). Every launch is asynchronous on that stream.
  *  - Element types are `tpp_dtype` codes. Accumulation is always fp32.
@@ -150,6 +152,21 @@ int tpp_qkv_rope_cache(const void *qkv, void *q_out, void *k_cache,
 int tpp_linear_act(const void *x, const void *w, const void *bias, void *y,
                    int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
                    int act, int dtype, void *stream);
+
+/* Plain GEMMs of tpp_linear_act (no bias, no activation) with at least as
+ * many 256 x 256 output tiles as the device has CUs run on hipBLASLt (zero
+ * workspace, plan cached per shape), as the reference runs its plain projections on
+ * nn.Linear (examples/LLM/fastqwen3.py:103-116); every other case, and any
+ * shape hipBLASLt cannot plan, runs on the MFMA kernels. enable = 0 keeps
+ * every GEMM on the MFMA kernels (also set by TPP_GEMM_VENDOR=0 in the
+ * environment), 1 restores the dispatch, a negative value only queries.
+ * Returns the previous setting. No counterpart in the reference: for
+ * comparing the two backends on one shape. */
+int tpp_gemm_vendor(int enable);
+
+/* Number of GEMMs hipBLASLt has run in this process (all devices). No
+ * counterpart in the reference: lets a test see which backend ran. */
+long long tpp_gemm_vendor_runs(void);
 
 /* Fused gate/up SwiGLU FFN projection, y[M, I] = T(silu(T(g))) * T(u) with
  * g = x . Wg^T, u = x . Wu^T, from one weight w_gu [2I, K] whose rows are

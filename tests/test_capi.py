@@ -91,3 +91,18 @@ def test_torchpp_alias_imports_reference_paths():
     import torchplusplus_amd.llmops.kvcache as real
 
     assert KVCache is real.KVCache
+
+
+def test_gemm_vendor_switch_returns_previous_setting():
+    L = _native.lib()
+    prev = L.tpp_gemm_vendor(-1)
+    try:
+        assert L.tpp_gemm_vendor(0) == prev
+        assert L.tpp_gemm_vendor(-1) == 0
+        assert L.tpp_gemm_vendor(1) == 0
+        assert L.tpp_gemm_vendor(7) == 1
+        assert L.tpp_gemm_vendor(-1) == 1
+    finally:
+        L.tpp_gemm_vendor(prev)
+    L.tpp_gemm_vendor_runs.restype = ctypes.c_longlong
+    assert L.tpp_gemm_vendor_runs() >= 0

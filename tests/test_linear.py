@@ -11,6 +11,32 @@ pytestmark = pytest.mark.gpu
 ACTS = {"none": 0, "gelu": 1, "silu": 2, "relu": 3}
 
 
+@pytest.fixture(params=["mfma", "vendor"])
+def backend(request):
+    """Plain GEMMs with at least one 256x256 tile per CU run on hipBLASLt unless
+    the dispatch is switched off: each such test runs once on the MFMA
+    kernels and once with the dispatch on. Yields a callable returning how
+    many GEMMs hipBLASLt has run so far."""
+    import ctypes
+    from torchplusplus_amd._native import lib
+    lb = lib()
+    lb.tpp_gemm_vendor_runs.restype = ctypes.c_longlong
+    prev = lb.tpp_gemm_vendor(1 if request.param == "vendor" else 0)
+    try:
+        yield request.param, lb.tpp_gemm_vendor_runs
+    finally:
+        lb.tpp_gemm_vendor(prev)
+
+
+def _expect_backend(backend, runs_before, m, n):
+    """The vendor path ran exactly when it was on and the shape has at least
+    one 256x256 tile per CU; never with the dispatch off."""
+    name, runs = backend
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    wanted = name == "vendor" and ((m + 255) // 256) * ((n + 255) // 256) >= cus
+    assert (runs() > runs_before) == wanted, f"{name} backend, {m}x{n}: hipBLASLt runs {runs() - runs_before}"
+
+
 def _mk(m, n, k, dtype, seed=0, wstd=0.02):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(m, k, generator=g).to(dtype)
@@ -74,29 +100,124 @@ def test_linear_pipelined_strided_output(dev):
 
 @pytest.mark.parametrize("m,n,k,dtype", [(5900, 4100, 128, torch.bfloat16), (8900, 2700, 64, torch.float16),
                                          (16384, 2048, 320, torch.bfloat16)])
-def test_linear_persistent_path(dev, m, n, k, dtype):
-    """256x256-tile launches with more tiles than CUs run one workgroup per CU
-    over its tiles, the K steps of consecutive tiles in one DMA stream:
-    ragged M and N (element-wise tail stores), one K step per tile (K = 64),
-    and blocks with 1, 2 and 2+ tiles."""
+def test_linear_persistent_path(dev, backend, m, n, k, dtype):
+    """256x256-tile launches with more tiles than CUs: on the MFMA kernels one
+    workgroup per CU loops over its tiles, the K steps of consecutive tiles in
+    one DMA stream (ragged M and N with element-wise tail stores, one K step
+    per tile at K = 64, blocks with 1, 2 and 2+ tiles); with the dispatch on,
+    hipBLASLt runs the same shapes."""
     x, w, _ = _mk(m, n, k, dtype, seed=23, wstd=0.05)
+    before = backend[1]()
     y = ext().linear(x.to(dev), w.to(dev), None, ACTS["none"])
-    close(y, oracle.linear_act(x, w, None, "none"), what=f"persistent {m}x{n}x{k}")
+    torch.cuda.synchronize()
+    _expect_backend(backend, before, m, n)
+    close(y, oracle.linear_act(x, w, None, "none"), what=f"persistent {m}x{n}x{k} {backend[0]}")
 
 
-def test_persistent_gemm_repeatable(dev):
+def test_persistent_gemm_repeatable(dev, backend):
     """The persistent kernel's first K step of a tile waits only for the DMA
     issued before the previous tile's output stores (vector memory completes
     in issue order): 40 back-to-back launches on the same operands must give
-    bit-identical outputs, equal to the oracle's within tolerance."""
+    bit-identical outputs, equal to the oracle's within tolerance. The same
+    holds for the hipBLASLt kernel the dispatch picks for this shape."""
     x, w, _ = _mk(16384, 2048, 512, torch.bfloat16, seed=26, wstd=0.05)
     xd, wd = x.to(dev), w.to(dev)
+    before = backend[1]()
     ref = ext().linear(xd, wd, None, ACTS["none"])
     outs = [ext().linear(xd, wd, None, ACTS["none"]) for _ in range(40)]
     torch.cuda.synchronize()
+    _expect_backend(backend, before, 16384, 2048)
     for i, y in enumerate(outs):
         assert torch.equal(y, ref), f"launch {i} differs"
-    close(ref, oracle.linear_act(x, w, None, "none"), what="persistent repeat")
+    close(ref, oracle.linear_act(x, w, None, "none"), what=f"persistent repeat {backend[0]}")
+
+
+@pytest.mark.parametrize("m,n,k,dtype", [(4352, 4096, 1024, torch.bfloat16), (4100, 4100, 1024, torch.float16),
+                                         (16384, 1024, 3072, torch.bfloat16)])
+def test_linear_vendor_matches_mfma(dev, m, n, k, dtype):
+    """A plain GEMM with at least one 256x256 tile per CU gives the same result
+    through hipBLASLt as through the MFMA kernel (both fp32 accumulation, one
+    rounding), each within tolerance of the oracle; the prefill down
+    projection's shape is the last case."""
+    import ctypes
+    from torchplusplus_amd._native import lib
+    lb = lib()
+    lb.tpp_gemm_vendor_runs.restype = ctypes.c_longlong
+    x, w, _ = _mk(m, n, k, dtype, seed=31, wstd=0.05)
+    xd, wd = x.to(dev), w.to(dev)
+    prev = lb.tpp_gemm_vendor(1)
+    try:
+        r0 = lb.tpp_gemm_vendor_runs()
+        y_v = ext().linear(xd, wd, None, ACTS["none"])
+        torch.cuda.synchronize()
+        assert lb.tpp_gemm_vendor_runs() == r0 + 1, "hipBLASLt did not run"
+        lb.tpp_gemm_vendor(0)
+        y_m = ext().linear(xd, wd, None, ACTS["none"])
+        torch.cuda.synchronize()
+        assert lb.tpp_gemm_vendor_runs() == r0 + 1
+    finally:
+        lb.tpp_gemm_vendor(prev)
+    ref = oracle.linear_act(x, w, None, "none")
+    close(y_v, ref, what=f"vendor {m}x{n}x{k}")
+    close(y_m, ref, what=f"mfma {m}x{n}x{k}")
+    # same inputs, two fp32-accumulating kernels: at most one rounding step apart
+    close(y_v, y_m, atol=1e-2, rtol=8e-3, what=f"vendor vs mfma {m}x{n}x{k}")
+
+
+def test_linear_vendor_in_graph(dev):
+    """A hipBLASLt GEMM captured into a HIP graph: every replay, with eager
+    work and a synchronisation between replays, equals the eager result."""
+    import ctypes
+    from torchplusplus_amd._native import lib
+    lb = lib()
+    lb.tpp_gemm_vendor_runs.restype = ctypes.c_longlong
+    x, w, _ = _mk(4352, 4096, 1024, torch.bfloat16, seed=33, wstd=0.05)
+    xd, wd = x.to(dev), w.to(dev)
+    prev = lb.tpp_gemm_vendor(1)
+    try:
+        y_e = ext().linear(xd, wd, None, ACTS["none"])  # eager: builds the plan
+        torch.cuda.synchronize()
+        r0 = lb.tpp_gemm_vendor_runs()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            y = ext().linear(xd, wd, None, ACTS["none"])
+        assert lb.tpp_gemm_vendor_runs() == r0 + 1, "hipBLASLt was not captured"
+        for r in range(4):
+            y.fill_(float(r + 1))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, y_e), f"replay {r} differs from the eager result"
+    finally:
+        lb.tpp_gemm_vendor(prev)
+    close(y_e, oracle.linear_act(x, w, None, "none"), what="vendor eager")
+
+
+def test_linear_vendor_pitched_output(dev):
+    """hipBLASLt path with an output row pitch (a column slice of a wider
+    tensor): the columns past N stay untouched."""
+    import ctypes
+    from torchplusplus_amd._native import lib
+    lb = lib()
+    lb.tpp_gemm_vendor_runs.restype = ctypes.c_longlong
+    x, w, _ = _mk(4352, 4096, 1024, torch.bfloat16, seed=32, wstd=0.05)
+    xd, wd = x.to(dev), w.to(dev)
+    out = torch.zeros(4352, 4104, dtype=torch.bfloat16, device=dev)
+    prev = lb.tpp_gemm_vendor(1)
+    try:
+        r0 = lb.tpp_gemm_vendor_runs()
+        rc = lb.tpp_linear_act(ctypes.c_void_p(xd.data_ptr()), ctypes.c_void_p(wd.data_ptr()), None,
+                               ctypes.c_void_p(out.data_ptr()), ctypes.c_int64(4352), ctypes.c_int64(4096),
+                               ctypes.c_int64(1024), ctypes.c_int64(1024), ctypes.c_int64(4104),
+                               ctypes.c_int(0), ctypes.c_int(1),
+                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert lb.tpp_gemm_vendor_runs() == r0 + 1, "hipBLASLt did not run"
+    finally:
+        lb.tpp_gemm_vendor(prev)
+    close(out[:, :4096], oracle.linear_act(x, w, None, "none"), what="vendor pitched output")
+    assert torch.count_nonzero(out[:, 4096:]) == 0
 
 
 @pytest.mark.parametrize("rows,inter,k", [(5200, 2400, 192), (16384, 3072, 128)])

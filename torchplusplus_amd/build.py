@@ -6,7 +6,8 @@ Produces, in-tree (so the files travel with the source tree):
 
 The reference built five CUDAExtension modules with nvcc for sm_80
 (/root/reference/setup.py:39-89). Here one hipcc invocation per source file
-targets gfx950 only; no CUTLASS/CK/hipBLASLt is compiled or linked.
+targets gfx950 only; no CUTLASS/CK is compiled. The library links ROCm's
+hipBLASLt for the plain GEMMs it dispatches there (csrc/gemm_lt.hip).
 
 Usage: python -m torchplusplus_amd.build  [--lib-only] [-j N]
 """
@@ -25,7 +26,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(REPO_DIR, "_build")
 LIB_NAME = "libtorchpp_hip.so"
 ARCH = os.environ.get("TORCHPP_ARCH", "gfx950")
-HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM_PATH = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.environ.get("HIPCC", os.path.join(ROCM_PATH, "bin", "hipcc"))
 
 # -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32; the host
 # pass prints a harmless "not a recognized feature" warning for it.
@@ -70,7 +72,9 @@ def build_lib(jobs: int = 8) -> str:
         list(ex.map(_run, cmds))
     out = os.path.join(PKG_DIR, LIB_NAME)
     tmp = out + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
+    rocm_lib = os.path.join(ROCM_PATH, "lib")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, f"-L{rocm_lib}", "-lhipblaslt",
+          f"-Wl,-rpath,{rocm_lib}", "-o", tmp])
     os.replace(tmp, out)
     return out
 

@@ -798,6 +798,11 @@ __global__ __launch_bounds__(256) void gemm_scalar_kernel(
   }
 }
 
+// hipBLASLt for plain GEMMs with at least one 256x256 tile per CU (gemm_lt.hip)
+bool lt_gemm_wanted(int64_t M, int64_t N, int cus);
+bool lt_gemm(const void *X, int64_t ldx, const void *W, int64_t ldw, void *Y, int64_t ldy,
+             int64_t M, int64_t N, int64_t K, bool bf16, hipStream_t st);
+
 template <typename T, int EPI, int ACT>
 static int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                        int64_t ldc, const void *bias, int64_t M, int64_t N, int64_t K,
@@ -805,6 +810,11 @@ static int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, v
   if (M == 0) return TPP_OK;
   const bool vec = (K % 8 == 0) && (lda % 8 == 0) && (ldb % 8 == 0) && aligned16(A) &&
                    aligned16(B);
+  if constexpr (EPI == kGPlain) {
+    if (vec && lt_gemm_wanted(M, N, device_cus()) &&
+        lt_gemm(A, lda, B, ldb, C, ldc, M, N, K, __is_same(T, bf16), st))
+      return check_launch(name);
+  }
   if (vec && K % 64 == 0 && M * N >= (int64_t)kDmaMinMN && lda <= kDmaMaxLd && ldb <= kDmaMaxLd) {
     if ((M + 127) / 128 * ((N + 127) / 128) > 0x7fffffffLL)
       return set_error(TPP_E_UNSUPPORTED, "%s: too many tiles", name);
