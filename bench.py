@@ -624,9 +624,10 @@ def measured_traffic(cache_len: int):
 def kernel_probe(name: str, reps: int = 5):
     """Counter runs (rocprofv3 --pmc ...) of one BASELINE config kernel:
     `gemm` = Linear+SiLU [2048x1024]x[3072x1024]^T + bias and the prefill
-    qkv GEMM [16384x1024]x[4096x1024]^T; `attn_prefill` = causal flash
+    qkv GEMM [16384x1024]x[4096x1024]^T, as dispatched (hipBLASLt) and on
+    the hand-written persistent kernel; `attn_prefill` = causal flash
     attention B4 S2048 16/8 d128. `reps` launches each, no timing."""
-    from torchplusplus_amd._native import ext
+    from torchplusplus_amd._native import ext, lib
 
     C = ext()
     dev = torch.device("cuda:0")
@@ -639,8 +640,13 @@ def kernel_probe(name: str, reps: int = 5):
         wp = (0.02 * torch.randn(4096, 1024, generator=g, device=dev)).bfloat16()
         for _ in range(reps):
             C.LinearSilu(x, w, b)
-        for _ in range(reps):
-            C.linear(xp, wp, None, 0)
+        for vendor in (1, 0):
+            prev = lib().tpp_gemm_vendor(vendor)
+            try:
+                for _ in range(reps):
+                    C.linear(xp, wp, None, 0)
+            finally:
+                lib().tpp_gemm_vendor(prev)
     elif name in ("attn_prefill", "attn_prefill_window"):
         q = torch.randn(4, 2048, 16, 128, generator=g, device=dev).bfloat16()
         k = torch.randn(4, 2048, 8, 128, generator=g, device=dev).bfloat16()
