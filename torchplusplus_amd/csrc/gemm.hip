@@ -234,6 +234,20 @@ template <int BK> __device__ __forceinline__ int swzk(int row) {
   else return (row >> 2) & 3;
 }
 
+// x[e] <- float(T(x[e])) for four values, converted two at a time (one
+// packed conversion per pair instead of one per value)
+template <typename T> __device__ __forceinline__ void round_pairs(float (&x)[4]) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef typename VecT<T>::v2 T2;
+#pragma unroll
+  for (int p = 0; p < 4; p += 2) {
+    const f2 in = {x[p], x[p + 1]};
+    const f2 out = __builtin_convertvector(__builtin_convertvector(in, T2), f2);
+    x[p] = out[0];
+    x[p + 1] = out[1];
+  }
+}
+
 template <typename T, int EPI, int ACT, int FM, int FN, int NST, int WM, int WN, int BK>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
     const T *__restrict__ A, int64_t lda, const T *__restrict__ B, int64_t ldb,
@@ -300,25 +314,25 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // bias of the wave's output columns (4 per lane per 8-column group),
-  // requested now so its latency hides under the main loop
-  typedef typename VecT<T>::v4 V4;
+  // The bias is added by one more MFMA per accumulator block after the K
+  // loop: A' = the bias of the block's 32 W rows in K column 0, B' = ones in
+  // K row 0, so acc += bias[n] . 1 with one fp32 rounding, the add of the
+  // epilogue formula, with no VALU work per output. Lane l < 32 holds
+  // bias[nw0 + 32 j + l] in element 0 of fragment j (requested now, so its
+  // latency hides under the main loop); every other element is zero.
   const int nw0 = n0 + wn * FN * 32; // first W row (output column before SwiGLU) of the wave
-  V4 bpre[EPI == kGBiasAct ? FN : 1][4];
+  V8 bfrag[EPI == kGBiasAct ? FN : 1];
   if constexpr (EPI == kGBiasAct) {
-    const bool bias_vec = (reinterpret_cast<uintptr_t>(bias) & 7) == 0;
+    if (bias) { // uniform
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j) {
+        const int c = nw0 + j * 32 + (lane & 31);
+        const T bv = bias[c < N ? c : N - 1];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c0 = nw0 + j * 32 + q * 8 + (lane >> 5) * 4;
-        if (bias && bias_vec && c0 + 4 <= N) {
-          bpre[j][q] = *reinterpret_cast<const V4 *>(bias + c0);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) bpre[j][q][e] = (bias && c0 + e < N) ? bias[c0 + e] : (T)0.0f;
-        }
+        for (int e = 0; e < 8; ++e) bfrag[j][e] = (T)0.0f;
+        bfrag[j][0] = (lane < 32 && c < N) ? bv : (T)0.0f;
       }
+    }
   }
 
   // Main loop. Each K tile is KS = BK/16 sub-steps of FM x FN MFMAs, with
@@ -394,6 +408,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
     }
   }
 
+  if constexpr (EPI == kGBiasAct) {
+    if (bias) {
+      V8 ones;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ones[e] = (T)0.0f;
+      ones[0] = lane < 32 ? (T)1.0f : (T)0.0f;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32<T>(bfrag[j], ones, acc[i][j]);
+    }
+  }
+
   // Epilogue. The operands are swapped in the MFMA (W rows first), so the
   // 32x32 accumulator holds lane -> output row m = i*32 + (lane & 31) and
   // registers 4q..4q+3 -> four consecutive output columns
@@ -415,26 +442,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int nl = j * 32 + q * 8 + half * 4; // wave-local W column of register 4q
-      float bv[4] = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (EPI == kGBiasAct) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bv[e] = to_f32(bpre[j][q][e]);
-      }
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         typename VecT<T>::v4 pk;
+        float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float v = acc[i][j][4 * q + e];
-          if constexpr (EPI == kGSwiGLU) {
-            const float gt = to_f32(from_f32<T>(v));
-            const float sl = to_f32(from_f32<T>(act_silu(gt)));
-            v = sl * to_f32(from_f32<T>(acc[i][j + 1][4 * q + e]));
-          } else if constexpr (EPI == kGBiasAct) {
-            v = apply_act<ACT>(to_f32(from_f32<T>(v + bv[e])));
-          }
-          pk[e] = from_f32<T>(v);
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
+        if constexpr (EPI == kGSwiGLU) {
+          float u[4], sl[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) u[e] = acc[i][j + 1][4 * q + e];
+          round_pairs<T>(v);
+          round_pairs<T>(u);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sl[e] = act_silu(v[e]);
+          round_pairs<T>(sl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = sl[e] * u[e];
+        } else if constexpr (EPI == kGBiasAct) {
+          round_pairs<T>(v); // the pre-activation rounded to T (bias already in acc)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = apply_act<ACT>(v[e]);
         }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pk[e] = from_f32<T>(v[e]);
         const int col = (EPI == kGSwiGLU) ? (j / 2) * 32 + q * 8 + half * 4 : nl;
         *reinterpret_cast<typename VecT<T>::v4 *>(stage + (i * 32 + ml) * LDR + col) = pk;
       }
