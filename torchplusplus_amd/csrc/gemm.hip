@@ -687,16 +687,23 @@ __global__ __launch_bounds__(512) void gemm_persist_kernel(
 #pragma unroll
           for (int i = 0; i < FM; ++i) {
             V4 pk;
+            float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              float v = acc[i][j][4 * q + e];
-              if constexpr (EPI == kGSwiGLU) {
-                const float gt = to_f32(from_f32<T>(v));
-                const float sl = to_f32(from_f32<T>(act_silu(gt)));
-                v = sl * to_f32(from_f32<T>(acc[i][j + 1][4 * q + e]));
-              }
-              pk[e] = from_f32<T>(v);
+            for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
+            if constexpr (EPI == kGSwiGLU) {
+              float u[4], sl[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) u[e] = acc[i][j + 1][4 * q + e];
+              round_pairs<T>(v);
+              round_pairs<T>(u);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) sl[e] = act_silu(v[e]);
+              round_pairs<T>(sl);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = sl[e] * u[e];
             }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pk[e] = from_f32<T>(v[e]);
             const int row = i * 32 + ml;
             const int col = ((EPI == kGSwiGLU) ? 0 : jj * 32) + q * 8 + half * 4; // column in the pass
             const int byte = row * RB + (((col * (int)sizeof(T)) / 16) ^ sw(row)) * 16 +
