@@ -793,7 +793,8 @@ def main():
         model.reset_kv_cache()
         model.forward_impl(ids, model.kv_cache_array, 0, last_only=True)
         torch.cuda.synchronize()
-        model.reset_kv_cache()
+        model.reset_kv_cache()  # zeroes the caches, as the reference's reset does
+        torch.cuda.synchronize()  # ... outside the timed prefill
         t0 = time.perf_counter()
         logits = model.forward_impl(ids, model.kv_cache_array, 0, last_only=True)
         torch.cuda.synchronize()
