@@ -11,16 +11,45 @@ pytestmark = pytest.mark.gpu
 
 # Model-level tolerance: each op meets atol 2e-2 / rtol 1e-2; through two bf16
 # decoder layers and the lm_head the per-op roundings compound (bf16 ulp at
-# |logit| ~ 1 is 7.8e-3), so single logits may differ by a few ulps. The
-# aggregate check (relative Frobenius error < 1e-2) is the tight one.
+# |logit| ~ 1 is 7.8e-3), so single bf16 logits may differ by a few ulps from
+# the bf16 oracle (which itself is up to ~4e-2 off an fp32 evaluation of the
+# same weights). The bf16 checks are therefore two-sided: per logit within
+# atol 6e-2 / rtol 2e-2 of the bf16 oracle, and no further from the fp32
+# evaluation than the bf16 oracle is (relative Frobenius error at most 1.25x
+# the oracle's own + 2e-3, largest logit error at most 1.5x + 5e-3). fp16
+# logits meet the north-star tolerance itself (measured: at most 0.2 of it).
 MODEL_ATOL, MODEL_RTOL = 6e-2, 2e-2
 
 
-def model_close(got, exp, what):
-    close(got, exp, atol=MODEL_ATOL, rtol=MODEL_RTOL, what=what)
-    g, e = got.float().cpu(), exp.float().cpu()
-    rel = ((g - e).norm() / e.norm()).item()
+def _rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def model_close(got, exp, what, exp32=None):
+    if got.dtype == torch.float16:
+        close(got, exp, what=what)  # atol 2e-2 / rtol 1e-2
+    else:
+        close(got, exp, atol=MODEL_ATOL, rtol=MODEL_RTOL, what=what)
+    rel = _rel(got, exp)
     assert rel < 1e-2, f"{what}: relative error {rel}"
+    if exp32 is not None:
+        e_gpu, e_orc = _rel(got, exp32), _rel(exp, exp32)
+        assert e_gpu <= 1.25 * e_orc + 2e-3, f"{what}: error vs fp32 {e_gpu:.5f}, oracle's own {e_orc:.5f}"
+        g, o, f = got.float().cpu(), exp.float().cpu(), exp32.float().cpu()
+        m_gpu, m_orc = (g - f).abs().max().item(), (o - f).abs().max().item()
+        assert m_gpu <= 1.5 * m_orc + 5e-3, f"{what}: max error vs fp32 {m_gpu:.4f}, oracle's own {m_orc:.4f}"
+
+
+def _oracle32(orc, cfg):
+    """fp32 evaluation of the oracle's (T-valued) weights, no rounding anywhere."""
+    cfg32 = QwenConfig(vocab_size=cfg.vocab_size, context_length=cfg.context_length,
+                       embed_dim=cfg.embed_dim, n_heads=cfg.n_heads, n_layers=cfg.n_layers,
+                       head_dim=cfg.head_dim, n_kv_heads=cfg.n_kv_heads, hidden_dim=cfg.hidden_dim,
+                       dtype=torch.float32)
+    o32 = Qwen3Oracle({}, cfg32, cfg.context_length)
+    o32.w = orc.w
+    return o32
 
 
 TINY = QwenConfig(vocab_size=1000, context_length=512, embed_dim=256, n_heads=4, n_layers=2,
@@ -47,17 +76,17 @@ def _model(dev, cfg=TINY, seed=0):
 def test_prefill_and_teacher_forced_decode(dev, cfg):
     m = _model(dev, cfg)
     orc = Qwen3Oracle(m.state_dict(), cfg, cfg.context_length)
+    o32 = _oracle32(orc, cfg)
     B, S = 3, 40
     ids = torch.randint(0, cfg.vocab_size, (B, S + 4), generator=torch.Generator().manual_seed(1))
     m.setup_kv_cache(64, B)
     m.reset_kv_cache()
     got = m.forward(ids[:, :S].to(dev), use_cache=True, cache_position=0)
-    exp = orc.forward(ids[:, :S], 0)
-    model_close(got, exp, "prefill logits")
+    model_close(got, orc.forward(ids[:, :S], 0), "prefill logits", o32.forward(ids[:, :S], 0))
     for t in range(4):  # decode with the true next token (teacher forcing)
-        got = m.forward(ids[:, S + t:S + t + 1].to(dev), use_cache=True, cache_position=S + t)
-        exp = orc.forward(ids[:, S + t:S + t + 1], S + t)
-        model_close(got, exp, f"decode step {t}")
+        step = ids[:, S + t:S + t + 1]
+        got = m.forward(step.to(dev), use_cache=True, cache_position=S + t)
+        model_close(got, orc.forward(step, S + t), f"decode step {t}", o32.forward(step, S + t))
 
 
 @torch.inference_mode()
