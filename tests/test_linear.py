@@ -193,6 +193,37 @@ def test_linear_vendor_in_graph(dev):
     close(y_e, oracle.linear_act(x, w, None, "none"), what="vendor eager")
 
 
+def test_linear_vendor_shape_first_met_under_capture(dev):
+    """A plain GEMM shape never run eagerly and first met inside a graph
+    capture runs on the MFMA kernel (no hipBLASLt plan is made during a
+    capture); its replays match the eager result, which then runs on
+    hipBLASLt."""
+    import ctypes
+    from torchplusplus_amd._native import lib
+    lb = lib()
+    lb.tpp_gemm_vendor_runs.restype = ctypes.c_longlong
+    m, n = 4352 + 256, 4096  # a shape no other test uses
+    x, w, _ = _mk(m, n, 1024, torch.bfloat16, seed=34, wstd=0.05)
+    xd, wd = x.to(dev), w.to(dev)
+    prev = lb.tpp_gemm_vendor(1)
+    try:
+        r0 = lb.tpp_gemm_vendor_runs()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            y = ext().linear(xd, wd, None, ACTS["none"])
+        assert lb.tpp_gemm_vendor_runs() == r0, "hipBLASLt planned a shape during capture"
+        g.replay()
+        torch.cuda.synchronize()
+        y_e = ext().linear(xd, wd, None, ACTS["none"])
+        torch.cuda.synchronize()
+        assert lb.tpp_gemm_vendor_runs() == r0 + 1, "eager call did not run on hipBLASLt"
+    finally:
+        lb.tpp_gemm_vendor(prev)
+    ref = oracle.linear_act(x, w, None, "none")
+    close(y, ref, what="captured (MFMA kernel)")
+    close(y_e, ref, what="eager (hipBLASLt)")
+
+
 def test_linear_vendor_pitched_output(dev):
     """hipBLASLt path with an output row pitch (a column slice of a wider
     tensor): the columns past N stay untouched."""
