@@ -22,7 +22,9 @@
 
 namespace tpp {
 
-enum NormMode { kRms = 0, kLayer = 1, kRmsStats = 2, kLayerStats = 3, kAddRms = 4 };
+// kLayer: LayerNorm with a bias, kLayerNB: without (no bias loads)
+enum NormMode { kRms = 0, kLayer = 1, kRmsStats = 2, kLayerStats = 3, kAddRms = 4, kLayerNB = 5 };
+constexpr bool layer_mode(int m) { return m == kLayer || m == kLayerNB || m == kLayerStats; }
 
 template <typename T, int LPR, int MAXV, int MODE>
 __global__ __launch_bounds__(256) void norm_rows_kernel(
@@ -46,7 +48,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
   // load, one round trip per chunk). The weight (and bias) chunks go with x,
   // so the output pass waits on no further memory.
   typedef typename VecT<T>::v8 V8;
-  constexpr bool kOut = (MODE == kRms || MODE == kLayer || MODE == kAddRms);
+  constexpr bool kOut = (MODE == kRms || MODE == kLayer || MODE == kLayerNB || MODE == kAddRms);
   V8 xr[MAXV], rr[MAXV], wr[MAXV], br[MAXV];
 #pragma unroll
   for (int j = 0; j < MAXV; ++j) {
@@ -55,7 +57,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
     xr[j] = ld_nt(reinterpret_cast<const V8 *>(x + rowc * ldx + cc));
     if constexpr (MODE == kAddRms) rr[j] = ld_nt(reinterpret_cast<const V8 *>(resid + rowc * ldy + cc));
     if constexpr (kOut) wr[j] = *reinterpret_cast<const V8 *>(w + cc);
-    if constexpr (MODE == kLayer) br[j] = *reinterpret_cast<const V8 *>((b ? b : w) + cc);
+    if constexpr (MODE == kLayer) br[j] = *reinterpret_cast<const V8 *>(b + cc);
   }
   __builtin_amdgcn_sched_barrier(0);
   float v[MAXV][8];
@@ -69,7 +71,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
       if constexpr (MODE == kAddRms) xv = to_f32(from_f32<T>(xv + to_f32(rr[j][i])));
       v[j][i] = ok ? xv : 0.f;
     }
-    if constexpr (MODE == kLayer || MODE == kLayerStats) {
+    if constexpr (layer_mode(MODE)) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) sum += v[j][i];
     } else {
@@ -80,7 +82,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
   sum = (LPR == kWave) ? wave_sum(sum) : row16_sum(sum);
 
   float scale, mean = 0.f;
-  if constexpr (MODE == kLayer || MODE == kLayerStats) {
+  if constexpr (layer_mode(MODE)) {
     mean = sum / (float)N;
     float sq = 0.f;
 #pragma unroll
@@ -126,11 +128,11 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(
       const int c = j * LPR + l;
       if (c < nvec) {
         float o[8];
-        if constexpr (MODE == kLayer) {
+        if constexpr (MODE == kLayer || MODE == kLayerNB) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
             o[i] = ((v[j][i] - mean) * scale) * to_f32(wr[j][i]);
-            if (b) o[i] += to_f32(br[j][i]);
+            if constexpr (MODE == kLayer) o[i] += to_f32(br[j][i]);
           }
         } else {
 #pragma unroll
@@ -169,11 +171,11 @@ __global__ __launch_bounds__(256) void norm_generic_kernel(
       v = to_f32(from_f32<T>(v + to_f32(resid[row * ldy + i])));
       resid[row * ldy + i] = from_f32<T>(v);
     }
-    sum += (MODE == kLayer || MODE == kLayerStats) ? v : v * v;
+    sum += layer_mode(MODE) ? v : v * v;
   }
   sum = block_sum(sum, red);
   float scale, mean = 0.f;
-  if constexpr (MODE == kLayer || MODE == kLayerStats) {
+  if constexpr (layer_mode(MODE)) {
     mean = sum / (float)N;
     float sq = 0.f;
     for (int i = threadIdx.x; i < N; i += blockDim.x) {
@@ -197,9 +199,9 @@ __global__ __launch_bounds__(256) void norm_generic_kernel(
     for (int i = threadIdx.x; i < N; i += blockDim.x) {
       float v = to_f32(src[i]);
       float o;
-      if constexpr (MODE == kLayer) {
+      if constexpr (MODE == kLayer || MODE == kLayerNB) {
         o = ((v - mean) * scale) * to_f32(w[i]);
-        if (b) o += to_f32(b[i]);
+        if constexpr (MODE == kLayer) o += to_f32(b[i]);
       } else {
         o = (v * scale) * to_f32(w[i]);
       }
@@ -316,8 +318,11 @@ extern "C" int tpp_layernorm(const void *x, const void *w, const void *b, void *
   if (!w || !y) return set_error(TPP_E_INVALID, "%s: null weight/output", name);
   if (ldy < N) return set_error(TPP_E_INVALID, "%s: output stride < N", name);
   return TPP_DISPATCH_HALF(dtype, [&] {
-    return launch_norm<T, kLayer>(x, w, b, y, nullptr, nullptr, nullptr, M, N, ldx,
-                                  ldy, eps, as_stream(stream), name);
+    if (b)
+      return launch_norm<T, kLayer>(x, w, b, y, nullptr, nullptr, nullptr, M, N, ldx,
+                                    ldy, eps, as_stream(stream), name);
+    return launch_norm<T, kLayerNB>(x, w, nullptr, y, nullptr, nullptr, nullptr, M, N, ldx,
+                                    ldy, eps, as_stream(stream), name);
   });
 }
 
