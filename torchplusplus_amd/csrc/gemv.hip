@@ -801,8 +801,25 @@ static bool launch_wide(const GemvArgs &a, hipStream_t st) {
 // row per wave 3.06 us, two or four rows per wave 3.7 / 4.5 us, a row split
 // over two waves with an LDS sum 3.14 us; the input through LDS instead of
 // read by every wave (6 MB of L2 reads per launch for 6 MB of weights),
-// 3.13-3.17 against 3.20-3.21 us in paired runs, the [1x1024] shape equal.)
+// 3.13-3.17 against 3.20-3.21 us in paired runs, the [1x1024] shape equal;
+// the products by v_dot2 instead of conversions and FMAs: 3.28 -> 3.19 us
+// and 2.97 -> 2.87 us cold.)
 constexpr int kB1MaxLoads = 8; // 16-byte weight loads per lane
+
+// acc + sum_e x[e] w[e] over 8 elements: four v_dot2 instructions (two
+// products each, accumulated in fp32) instead of 16 conversions and 8 FMAs
+template <typename T>
+__device__ __forceinline__ float dot8(const typename VecT<T>::v8 &x, const typename VecT<T>::v8 &w,
+                                      float acc) {
+  typedef typename VecT<T>::v2 T2;
+#pragma unroll
+  for (int p = 0; p < 8; p += 2) {
+    const T2 a = {x[p], x[p + 1]}, b = {w[p], w[p + 1]};
+    if constexpr (__is_same(T, bf16)) acc = __builtin_amdgcn_fdot2_f32_bf16(a, b, acc, false);
+    else acc = __builtin_amdgcn_fdot2(a, b, acc, false);
+  }
+  return acc;
+}
 
 template <typename T, int EPI, int ACT, int CPL>
 __global__ __launch_bounds__(1024) void gemv_b1_kernel(GemvArgs a) {
@@ -837,10 +854,12 @@ __global__ __launch_bounds__(1024) void gemv_b1_kernel(GemvArgs a) {
   float acc = 0.f;
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
-    const V8 xv = s_x[i * 64 + lane];
-    const float on = lane + 64 * i < nch ? 1.f : 0.f;
+    V8 xv = s_x[i * 64 + lane];
+    if (lane + 64 * i >= nch) { // a chunk past the row: x read as zeros
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += (on * to_f32(xv[e])) * to_f32(wr[i][e]);
+      for (int e = 0; e < 8; ++e) xv[e] = (T)0.0f;
+    }
+    acc = dot8<T>(xv, wr[i], acc);
   }
   acc = wave_sum(acc);
   if (lane == 0) {
