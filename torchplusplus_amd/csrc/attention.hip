@@ -1032,20 +1032,25 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
   float c[8], sn[8];
   cs_vals(c_lo, c_hi, fz.cs_dtype, c);
   cs_vals(s_lo, s_hi, fz.cs_dtype, sn);
-  float qv[G][8];
+  // q rounded to T after the fused QK-norm and RoPE, as the unfused path
+  // stores it in its q tensor; scores by v_dot2 on T pairs accumulated in
+  // fp32, scaled after the row reduction
+  V8 qh[G];
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) {
+    float qv[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qv[gi][j] = to_f32(q_raw[gi][j]);
+    for (int j = 0; j < 8; ++j) qv[j] = to_f32(q_raw[gi][j]);
     if (fused) {
       float wq[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) wq[j] = to_f32(qw_raw[j]);
-      norm_rope_vals<T, LPK>(qv[gi], fz.qw != nullptr, wq, fz.eps, c, sn, dp);
+      norm_rope_vals<T, LPK>(qv, fz.qw != nullptr, wq, fz.eps, c, sn, dp);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qv[gi][j] *= p.scale_log2;
+    for (int j = 0; j < 8; ++j) qh[gi][j] = from_f32<T>(qv[j]);
   }
+  const float qscale = p.scale_log2;
   // the new token's K (normalised, rotated) and V, computed here by every
   // wave and pinned (empty asm uses): left to the block that appends them
   // they would keep their loads in flight across the whole key loop, and the
@@ -1076,19 +1081,14 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool ok = (unsigned)(base + u * NW * KPW + row - k_begin) < (unsigned)(k_end - k_begin);
-      float kf[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) kf[j] = to_f32(kr[u][j]);
 #pragma unroll
       for (int gi = 0; gi < G; ++gi) {
-        float sdot = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sdot += qv[gi][j] * kf[j];
+        float sdot = dot8<T>(qh[gi], kr[u], 0.f);
         sdot += dpp_f32<kDppQuadXor1>(sdot);
         sdot += dpp_f32<kDppQuadXor2>(sdot);
         if constexpr (LPK >= 8) sdot += dpp_f32<kDppRowHalfMirror>(sdot);
         if constexpr (LPK >= 16) sdot += dpp_f32<kDppRowMirror>(sdot);
-        sc[u][gi] = ok ? sdot : -INFINITY;
+        sc[u][gi] = ok ? sdot * qscale : -INFINITY;
       }
     }
 #pragma unroll
@@ -1144,12 +1144,12 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs p, const 
       store8((T *)kp + (int64_t)pnew * p.k_ss, kf);
       store8((T *)vp + (int64_t)pnew * p.v_ss, vf);
     }
+    V8 kh; // the key as the cache holds it
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kh[j] = from_f32<T>(kf[j]);
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
-      float sdot = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sdot += qv[gi][j] * kf[j];
-      sdot = group_sum<LPK>(sdot);
+      const float sdot = group_sum<LPK>(dot8<T>(qh[gi], kh, 0.f)) * qscale;
       if (row == 0) {
         const float mn = fmaxf(m[gi], sdot);
         const float a = exp2f(m[gi] - mn), e = exp2f(sdot - mn);

@@ -806,20 +806,6 @@ static bool launch_wide(const GemvArgs &a, hipStream_t st) {
 // and 2.97 -> 2.87 us cold.)
 constexpr int kB1MaxLoads = 8; // 16-byte weight loads per lane
 
-// acc + sum_e x[e] w[e] over 8 elements: four v_dot2 instructions (two
-// products each, accumulated in fp32) instead of 16 conversions and 8 FMAs
-template <typename T>
-__device__ __forceinline__ float dot8(const typename VecT<T>::v8 &x, const typename VecT<T>::v8 &w,
-                                      float acc) {
-  typedef typename VecT<T>::v2 T2;
-#pragma unroll
-  for (int p = 0; p < 8; p += 2) {
-    const T2 a = {x[p], x[p + 1]}, b = {w[p], w[p + 1]};
-    if constexpr (__is_same(T, bf16)) acc = __builtin_amdgcn_fdot2_f32_bf16(a, b, acc, false);
-    else acc = __builtin_amdgcn_fdot2(a, b, acc, false);
-  }
-  return acc;
-}
 
 template <typename T, int EPI, int ACT, int CPL>
 __global__ __launch_bounds__(1024) void gemv_b1_kernel(GemvArgs a) {

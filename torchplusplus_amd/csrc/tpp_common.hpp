@@ -48,6 +48,21 @@ template <> struct VecT<bf16> {
   typedef bf16x2 v2;
 };
 
+// acc + sum_e x[e] w[e] over 8 elements: four v_dot2 instructions (two
+// products each, accumulated in fp32) instead of 16 conversions and 8 FMAs
+template <typename T>
+__device__ __forceinline__ float dot8(const typename VecT<T>::v8 &x, const typename VecT<T>::v8 &w,
+                                      float acc) {
+  typedef typename VecT<T>::v2 T2;
+#pragma unroll
+  for (int p = 0; p < 8; p += 2) {
+    const T2 a = {x[p], x[p + 1]}, b = {w[p], w[p + 1]};
+    if constexpr (__is_same(T, bf16)) acc = __builtin_amdgcn_fdot2_f32_bf16(a, b, acc, false);
+    else acc = __builtin_amdgcn_fdot2(a, b, acc, false);
+  }
+  return acc;
+}
+
 __device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
 __device__ __forceinline__ float to_f32(float x) { return x; }
