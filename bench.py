@@ -817,9 +817,13 @@ def main():
         decode_s = time.perf_counter() - t0
         log(f"[bench] decode {K} steps {decode_s * 1e3:.2f} ms")
         tok_s = BATCH * K / decode_s
+        # the one-launch decode kernels flag a bounded wait that gave up (their
+        # output is then wrong): such a run measured nothing valid
+        model.check_device_errors()
 
         L = PREFILL + K // 2  # mean cache length over the timed steps
         kernels, attn_us, attn_bytes = measure_kernels(model, dec, cfg, L)
+        model.check_device_errors()
         log("[bench] kernel table done")
         configs = measure_configs()
         log("[bench] config table done")
