@@ -18,7 +18,10 @@
 // on first use. A shape whose heuristic returns nothing, or whose matmul
 // call fails, is remembered and runs on the hand-written kernel. Nothing is
 // created while the stream is being captured into a graph: an uncached shape
-// met under capture runs on the hand-written kernel.
+// met under capture runs on the hand-written kernel. At most kLtMaxPlans
+// shapes are kept per device (M changes with every prompt length in
+// serving); shapes past that run on the hand-written kernel, with no
+// heuristic query on the host.
 #include "tpp_common.hpp"
 
 #include <hipblaslt/hipblaslt.h>
@@ -50,6 +53,7 @@ struct LtDevice {
 };
 
 constexpr int kLtMaxDevices = 64;
+constexpr size_t kLtMaxPlans = 512;
 std::mutex g_lt_mu;
 LtDevice g_lt[kLtMaxDevices];
 
@@ -133,7 +137,7 @@ bool lt_gemm(const void *X, int64_t ldx, const void *W, int64_t ldw, void *Y, in
   const LtKey key(bf16 ? 1 : 0, M, N, K, ldx, ldw, ldy);
   auto it = d.plans.find(key);
   if (it == d.plans.end()) {
-    if (capturing) return false;
+    if (capturing || d.plans.size() >= kLtMaxPlans) return false;
     it = d.plans.emplace(key, make_plan(d.handle, bf16 ? HIP_R_16BF : HIP_R_16F, M, N, K, ldx, ldw, ldy))
              .first;
   }
